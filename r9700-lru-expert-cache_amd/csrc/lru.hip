@@ -1,0 +1,748 @@
+// Device-side LRU expert cache for gfx950 (MI355X): the manager, the fused manager +
+// moe_align_block_size, and the miss gather.
+//
+// Semantics are those of kernels/lru/r4d_lru.hip (lru_manage_k :187-269, pickVictims :119-185,
+// lru_fused_k :418-575, lru_gather_k :271-301); the entry points at the bottom keep its C-ABI.
+// The implementation is this build's own, shaped for wave64 CDNA4:
+//
+//  * One workgroup of 256 threads (one wave per SIMD), five barriers for the fused kernel
+//    (three for the manager). Every global load is issued up front, so the kernel pays one
+//    memory round trip, not one per phase; the align outputs are pre-filled with their
+//    sentinels by coalesced stores in the same window, and only the first barrier waits for
+//    global stores (the rest order LDS only).
+//  * Cross-lane reductions and scans are DPP + v_readlane (wave-uniform scalars), not LDS
+//    shuffles.
+//  * Routed / non-resident sets are 64-bit-word bitmaps built from wave ballots; misses are
+//    ranked in ascending expert id by popcount prefixes (no block scan).
+//  * Victims -- the nins smallest (stamp << 20 | slot) keys among slots whose expert is not
+//    routed, ascending -- are chosen by ONE wave with no barrier: a radix-style search for the
+//    nins-th smallest key (one ballot + popcount per slot register per key bit), a ballot
+//    compaction of the keys at or below it, and a rank of the <= nins survivors among
+//    themselves. Cost grows with key bits and nins, never with a per-insert block reduction,
+//    so there is no insert-count cliff.
+//  * Align is stable at every mk: a token's rank inside its bucket is the number of earlier
+//    tokens routed to the same expert, from a bit-sliced wave match plus per-wave counts in
+//    LDS.
+//
+// Preconditions (checked by the reference's own tests after every step, tests/lru/test_lru.py:
+// 138-145): table/map_cold complementary, table[slot_expert[s]] == s for resident slots,
+// entries in range. Under them the results equal the reference kernel's bit for bit.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "rlu.h"
+#include "wave.h"
+
+namespace rlu {
+
+constexpr int NT = 256;
+constexpr int NW = NT / WAVE;
+constexpr int MAXS = 1024;
+constexpr int MAXE = 1024;
+constexpr int MAXINS = 1024;
+constexpr int SLOT_BITS = 20;
+constexpr int QS = MAXS / WAVE;      // slot registers per lane in the selecting wave
+constexpr int EJ = MAXE / NT;        // experts per thread
+constexpr int NWORD = MAXE / 64;     // bitmap words
+
+constexpr int TW = NT / 64;          // u64 words of a per-expert token mask (<= NT tokens)
+constexpr int LSTAGE = 4096;         // align outputs staged in LDS up to this many sorted ids
+constexpr int NBSTAGE = 256;         // ... and this many expert ids, per side
+
+struct LruLds {
+  uint64_t rbits[NWORD];             // routed this step (by expert)
+  uint64_t nres[NWORD];              // table[e] < 0 on entry (by expert)
+  uint64_t sbusy[NWORD];             // the slot's expert is routed this step (by slot)
+  int mpre[NWORD];                   // misses in earlier bitmap words
+  int misc[4];                       // nact, nins
+  int tab[MAXE];                     // table on entry
+  int ecnt[MAXE];                    // general path: tokens per expert, then the per-expert
+                                     // base of the token chunk being placed
+  int vslot[MAXINS];                 // victim slot of rank r
+  int vold[MAXINS];                  // expert evicted from it (or -1)
+  uint64_t vkey[MAXINS];             // victims, compacted, before ranking
+  int vpack[MAXINS];                 // (slot << 16) | (old expert & 0xffff), same order
+  int cnt_h[MAXS];                   // post-update tokens per hot bucket (slot)
+  int hexp[MAXS];                    // post-update expert of a hot bucket with tokens
+  int cnt_c[MAXE];                   // post-update tokens per cold bucket (expert)
+  int cum_h[MAXS];
+  int cum_c[MAXE];
+  int wsum[NW][2];
+  union {
+    uint64_t tmask[MAXE][TW];        // staged path: bit i of expert e = token i routes to e
+    uint8_t wcnt[NW][MAXE];          // general path: tokens per (wave, expert) in a chunk
+  } tk;
+  int stage_h[LSTAGE], stage_c[LSTAGE];
+  int stage_eh[NBSTAGE], stage_ec[NBSTAGE];
+};
+
+__device__ __forceinline__ bool bit_of(const uint64_t* bm, int e) {
+  return ((bm[e >> 6] >> (e & 63)) & 1ull) != 0;
+}
+
+// ---- victim selection (one wave) ------------------------------------------------------
+// Victims are the nact smallest (stamp, slot) pairs among evictable slots, ascending; rank r
+// installs miss r. Stamps are split into the oldest group (stamp == smin) and the rest:
+//   * if the oldest group alone has >= nact slots (always at nact == 1, and the usual case
+//     in steady state, where a whole step's hits share one stamp), the victims are its first
+//     nact slots in slot order -- no search, no ranking;
+//   * otherwise a two-bit-per-round search over the stamp range finds the boundary stamp tau
+//     (#{stamp < tau} < nact <= #{stamp <= tau}); the boundary group is cut in slot order by
+//     ballot prefix, and the <= nact survivors are ranked among themselves.
+// Stamps outside [0, 2^43) fall back to a search over the reference key (stamp << 20) | slot
+// itself (biased to unsigned order), which the reference defines with wrap-around.
+
+// writes victim of rank p
+__device__ __forceinline__ void put_victim(LruLds& L, int p, int slot, int old) {
+  L.vslot[p] = slot;
+  L.vold[p] = old;
+}
+
+// rank the n compacted keys L.vkey[0..n) among themselves (keys unique), then install
+__device__ __forceinline__ void rank_compacted(LruLds& L, int n) {
+  wave_lds_sync();
+  for (int p = lane_id(); p < n; p += WAVE) {
+    const uint64_t v = L.vkey[p];
+    int r = 0;
+    int j = 0;
+    for (; j + 4 <= n; j += 4)
+      r += (L.vkey[j] < v) + (L.vkey[j + 1] < v) + (L.vkey[j + 2] < v) + (L.vkey[j + 3] < v);
+    for (; j < n; ++j) r += (L.vkey[j] < v);
+    const int pk = L.vpack[p];
+    put_victim(L, r, pk >> 16, (int)(short)(pk & 0xffff));
+  }
+}
+
+template <int Q>
+__device__ __forceinline__ void compact_victims(LruLds& L, const bool* vic, const uint64_t* key,
+                                                const int* se) {
+  const int lane = lane_id();
+  int base = 0;
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    const uint64_t m = __ballot(vic[q]);
+    if (vic[q]) {
+      const int p = base + mbcnt(m);
+      L.vkey[p] = key[q];
+      L.vpack[p] = ((lane + WAVE * q) << 16) | (se[q] & 0xffff);
+    }
+    base += __popcll(m);
+  }
+}
+
+template <int Q>
+__device__ __forceinline__ int select_victims(LruLds& L, int S, int nins, const int* se,
+                                              const long long* sst, const bool* ev) {
+  const int lane = lane_id();
+  int nev = 0;
+  bool wide = false;
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    nev += __popcll(__ballot(ev[q]));
+    wide |= ev[q] && (sst[q] >> 32) != 0;
+  }
+  const int nact = nins < nev ? nins : nev;
+  if (nact == 0) return 0;
+
+  if (!__ballot(wide)) {
+    // ---- every evictable stamp fits 32 bits -------------------------------------------------
+    uint32_t mn = ~0u, mx = 0;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      const uint32_t x = (uint32_t)sst[q];
+      if (ev[q]) {
+        mn = x < mn ? x : mn;
+        mx = x > mx ? x : mx;
+      }
+    }
+    mn = (uint32_t)(~wave_reduce64(~(uint64_t)mn, OpMax64()) );   // min via max of complement
+    mx = (uint32_t)wave_reduce64((uint64_t)mx, OpMax64());
+    uint64_t g[Q];
+    int cnt0 = 0;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      g[q] = __ballot(ev[q] && (uint32_t)sst[q] == mn);
+      cnt0 += __popcll(g[q]);
+    }
+    if (cnt0 >= nact) {
+      // all victims from the oldest group, in slot order
+      int base = 0;
+#pragma unroll
+      for (int q = 0; q < Q; ++q) {
+        const int p = base + mbcnt(g[q]);
+        if (((g[q] >> lane) & 1ull) && p < nact) put_victim(L, p, lane + WAVE * q, se[q]);
+        base += __popcll(g[q]);
+      }
+      return nact;
+    }
+    // boundary stamp: tau = largest rel with #{rel < tau} < nact (two bits per round)
+    uint32_t rel[Q];
+#pragma unroll
+    for (int q = 0; q < Q; ++q) rel[q] = ev[q] ? (uint32_t)sst[q] - mn : ~0u;
+    int b = 32 - __clz(mx - mn);                    // mx > mn here: cnt0 < nact <= nev
+    uint32_t tau = 0;
+    if (b & 1) {
+      --b;
+      const uint32_t c1 = tau | (1u << b);
+      int n1 = 0;
+#pragma unroll
+      for (int q = 0; q < Q; ++q) n1 += __popcll(__ballot(rel[q] < c1));
+      if (n1 < nact) tau = c1;
+    }
+    while (b > 0) {
+      b -= 2;
+      const uint32_t u = 1u << b;
+      const uint32_t c1 = tau + u, c2 = tau + 2 * u, c3 = tau + 3 * u;
+      int n1 = 0, n2 = 0, n3 = 0;
+#pragma unroll
+      for (int q = 0; q < Q; ++q) {
+        n1 += __popcll(__ballot(rel[q] < c1));
+        n2 += __popcll(__ballot(rel[q] < c2));
+        n3 += __popcll(__ballot(rel[q] < c3));
+      }
+      tau += (uint32_t)((n1 < nact) + (n2 < nact) + (n3 < nact)) * u;
+    }
+    int clt = 0;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) clt += __popcll(__ballot(rel[q] < tau));
+    const int need = nact - clt;                    // >= 1 taken from the tau group
+    bool vic[Q];
+    uint64_t key[Q];
+    int base = 0;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      const uint64_t m = __ballot(rel[q] == tau);
+      const int p = base + mbcnt(m);
+      vic[q] = rel[q] < tau || (rel[q] == tau && p < need);
+      key[q] = ((uint64_t)rel[q] << 10) | (uint64_t)(lane + WAVE * q);
+      base += __popcll(m);
+    }
+    compact_victims<Q>(L, vic, key, se);
+    rank_compacted(L, nact);
+    return nact;
+  }
+
+  // ---- general: search the reference key (stamp << 20) | slot, biased to unsigned ----------
+  const uint64_t bias = 0x8000000000000000ull;
+  uint64_t rel[Q];
+  uint64_t lo = ~0ull, hi = 0;
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    const uint64_t k = (((uint64_t)sst[q] << SLOT_BITS) | (uint64_t)(lane + WAVE * q)) ^ bias;
+    rel[q] = ev[q] ? k : ~0ull;
+    if (ev[q]) {
+      lo = k < lo ? k : lo;
+      hi = k > hi ? k : hi;
+    }
+  }
+  lo = wave_reduce64(lo, OpMin64());
+  hi = wave_reduce64(hi, OpMax64());
+#pragma unroll
+  for (int q = 0; q < Q; ++q)
+    if (ev[q]) rel[q] -= lo;
+  const uint64_t span = hi - lo;
+  int b = span ? 64 - __clzll(span) : 0;
+  uint64_t T = 0;
+  for (; b > 0; --b) {
+    const uint64_t c1 = T | (1ull << (b - 1));
+    int n1 = 0;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) n1 += __popcll(__ballot(rel[q] < c1));
+    if (n1 < nact) T = c1;
+  }
+  bool vic[Q];
+#pragma unroll
+  for (int q = 0; q < Q; ++q) vic[q] = ev[q] && rel[q] <= T;
+  compact_victims<Q>(L, vic, rel, se);
+  rank_compacted(L, nact);
+  return nact;
+}
+
+// Wave 0 after the routed set is known: refresh the stamps of hit slots, then pick victims.
+template <int Q>
+__device__ __forceinline__ int wave0_slots(LruLds& L, int S, int nins, bool ins_ok,
+                                           long long st, long long* __restrict__ slot_stamp,
+                                           const int (&se)[QS], const long long (&sst)[QS]) {
+  const int lane = lane_id();
+  uint64_t sb[Q];
+#pragma unroll
+  for (int q = 0; q < Q; ++q) sb[q] = L.sbusy[q];   // uniform reads, one round trip
+  bool ev[Q];
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    const int i = lane + WAVE * q;
+    const bool busy = i < S && ((sb[q] >> lane) & 1ull);
+    if (ins_ok && busy) slot_stamp[i] = st;   // hit: r4d_lru.hip:228-238
+    ev[q] = i < S && !busy;
+  }
+  if (!ins_ok || nins == 0) return 0;
+  return select_victims<Q>(L, S, nins, se, sst, ev);
+}
+
+__device__ __forceinline__ int wave0_dispatch(LruLds& L, int S, int nins, bool ins_ok,
+                                              long long st, long long* __restrict__ slot_stamp,
+                                              const int (&se)[QS], const long long (&sst)[QS]) {
+  switch ((S + WAVE - 1) / WAVE) {
+#define RLU_Q(n) \
+  case n: return wave0_slots<n>(L, S, nins, ins_ok, st, slot_stamp, se, sst);
+    RLU_Q(1) RLU_Q(2) RLU_Q(3) RLU_Q(4) RLU_Q(5) RLU_Q(6) RLU_Q(7) RLU_Q(8)
+    RLU_Q(9) RLU_Q(10) RLU_Q(11) RLU_Q(12) RLU_Q(13) RLU_Q(14) RLU_Q(15) RLU_Q(16)
+#undef RLU_Q
+    default: return 0;
+  }
+}
+
+// block-size arithmetic: shifts when bs is a power of two (always, in practice: 16)
+struct Blk {
+  int bs, sh;
+  __device__ Blk(int b) : bs(b), sh((b & (b - 1)) == 0 ? __builtin_ctz(b) : -1) {}
+  __device__ __forceinline__ int pad(int c) const {
+    return sh >= 0 ? ((c + bs - 1) >> sh) << sh : (c + bs - 1) / bs * bs;
+  }
+  __device__ __forceinline__ int blk(int x) const { return sh >= 0 ? x >> sh : x / bs; }
+};
+
+// Align output helpers, called with either the LDS stage or the global outputs so that
+// each call site compiles to LDS or global stores (no generic pointers).
+__device__ __forceinline__ void fill_align(int* __restrict__ oh, int* __restrict__ oc,
+                                           int* __restrict__ eh, int* __restrict__ ec, int Lsz,
+                                           int NB, int mk) {
+  for (int k = threadIdx.x; k < Lsz; k += NT) {
+    oh[k] = mk;
+    oc[k] = mk;
+  }
+  for (int k = threadIdx.x; k < NB; k += NT) {
+    eh[k] = -1;
+    ec[k] = -1;
+  }
+}
+
+// The expert ids of a thread's buckets and, when `tokens`, each bucket's tokens in index
+// order (from the per-expert token masks).
+__device__ __forceinline__ void place_buckets(LruLds& L, int* __restrict__ oh,
+                                              int* __restrict__ oc, int* __restrict__ eh,
+                                              int* __restrict__ ec, const int (&ph)[EJ],
+                                              const int (&pc)[EJ], int h0, int h1, int c0,
+                                              int c1, int runa, int runb, int NB, const Blk& B,
+                                              bool tokens) {
+#pragma unroll
+  for (int side = 0; side < 2; ++side) {
+    const bool hs = side == 0;
+    int run = hs ? runa : runb;
+    const int i0 = hs ? h0 : c0, i1 = hs ? h1 : c1;
+#pragma unroll
+    for (int j = 0; j < EJ; ++j) {
+      const int c = hs ? ph[j] : pc[j];
+      const int i = i0 + j;
+      if (i < i1) {
+        if (hs)
+          L.cum_h[i] = run;
+        else
+          L.cum_c[i] = run;
+        if (c > 0) {
+          int* eo = hs ? eh : ec;
+          for (int k = B.blk(run); k < B.blk(run + B.pad(c)); ++k)
+            if (k < NB) eo[k] = i;
+          if (tokens) {
+            int* so = hs ? oh : oc;
+            const int x = hs ? L.hexp[i] : i;
+            int p = run;
+#pragma unroll
+            for (int wd = 0; wd < TW; ++wd) {
+              uint64_t m = L.tk.tmask[x][wd];
+              while (m) {
+                so[p++] = wd * 64 + __ffsll((long long)m) - 1;
+                m &= m - 1;
+              }
+            }
+          }
+        }
+        run += B.pad(c);
+      }
+    }
+  }
+}
+
+template <bool ALIGN>
+__global__ __launch_bounds__(NT) void lru_k(
+    const int* __restrict__ ids, int mk, int E, int S, int max_distinct, int max_inserts,
+    int* __restrict__ table, int* __restrict__ map_cold, int* __restrict__ slot_expert,
+    long long* __restrict__ slot_stamp, unsigned char* __restrict__ routed,
+    long long* __restrict__ step, int* __restrict__ miss, int* __restrict__ n_miss, int bs,
+    int Lsz, int NB, int* __restrict__ sorted_hot, int* __restrict__ eids_hot,
+    int* __restrict__ npad_hot, int* __restrict__ sorted_cold, int* __restrict__ eids_cold,
+    int* __restrict__ npad_cold) {
+  __shared__ LruLds L;
+  const int t = threadIdx.x;
+  const int w = t / WAVE;
+  const int lane = lane_id();
+  // Decode-sized calls stage both align outputs in LDS, so every output element is written
+  // to global memory exactly once, by coalesced stores at the end. Larger ones pre-fill the
+  // outputs in global memory and overwrite them after a full barrier.
+  const bool staged = ALIGN && mk <= NT && Lsz <= LSTAGE && NB <= NBSTAGE;
+
+  // ---- loads, all issued before any barrier --------------------------------------------
+  const long long st = step[0] + 1;
+  int tab[EJ];
+#pragma unroll
+  for (int j = 0; j < EJ; ++j) {
+    const int e = t + NT * j;
+    tab[j] = e < E ? table[e] : 0;
+  }
+  int se[QS];
+  long long sst[QS];
+  if (w == 0) {
+#pragma unroll
+    for (int q = 0; q < QS; ++q) {
+      const int i = lane + WAVE * q;
+      se[q] = i < S ? slot_expert[i] : -1;
+      sst[q] = i < S ? slot_stamp[i] : 0;
+    }
+  }
+  const int tok0 = t < mk ? ids[t] : -1;
+  const bool v0 = tok0 >= 0 && tok0 < E;
+
+  // ---- init -------------------------------------------------------------------------------
+  if (ALIGN) {
+    if (staged) {
+      if (v0) {                                  // clear the masks this step will use
+#pragma unroll
+        for (int x = 0; x < TW; ++x) L.tk.tmask[tok0][x] = 0;
+      }
+      fill_align(L.stage_h, L.stage_c, L.stage_eh, L.stage_ec, Lsz, NB, mk);
+    } else {
+      reinterpret_cast<uint4*>(&L.tk.wcnt[0][0])[t] = make_uint4(0, 0, 0, 0);
+      fill_align(sorted_hot, sorted_cold, eids_hot, eids_cold, Lsz, NB, mk);
+    }
+    for (int i = t; i < S; i += NT) L.cnt_h[i] = 0;
+  }
+#pragma unroll
+  for (int j = 0; j < EJ; ++j) {
+    const int e = t + NT * j;
+    const uint64_t nr = __ballot(e < E && tab[j] < 0);
+    if (lane == 0) L.nres[j * NW + w] = nr;
+    if (e < E) {
+      L.tab[e] = tab[j];
+      L.ecnt[e] = 0;
+    }
+  }
+  if (t < NWORD) {
+    L.rbits[t] = 0;
+    L.sbusy[t] = 0;
+  }
+  if (ALIGN && !staged)
+    __syncthreads();  // 1 -- full: the global sentinel stores complete before any overwrite
+  else
+    lds_barrier();    // 1
+
+  // ---- mark routed experts and their slots; per-expert token sets -------------------------
+  for (int i = t; i < mk; i += NT) {
+    const int e = i == t ? tok0 : ids[i];
+    if (e >= 0 && e < E) {
+      atomicOr(reinterpret_cast<unsigned long long*>(&L.rbits[e >> 6]), 1ull << (e & 63));
+      const int s = L.tab[e];
+      if ((unsigned)s < (unsigned)S)
+        atomicOr(reinterpret_cast<unsigned long long*>(&L.sbusy[s >> 6]), 1ull << (s & 63));
+      if (ALIGN) {
+        if (staged)
+          atomicOr(reinterpret_cast<unsigned long long*>(&L.tk.tmask[e][i >> 6]),
+                   1ull << (i & 63));
+        else
+          atomicAdd(&L.ecnt[e], 1);
+      }
+    }
+  }
+  const int kbits = E > 1 ? 32 - __clz(E - 1) : 0;
+  int inrank = 0;
+  if (ALIGN && !staged) {
+    const uint64_t m = match_any(tok0, v0, kbits);
+    inrank = mbcnt(m);
+    if (v0 && inrank == 0) L.tk.wcnt[w][tok0] = (uint8_t)__popcll(m);
+  }
+  lds_barrier();  // 2
+
+  // ---- wave 0: distinct count, miss ranks, stamp refresh, victims --------------------------
+  if (w == 0) {
+    uint64_t rw = 0, nw = 0;
+    if (lane < NWORD) {
+      rw = L.rbits[lane];
+      nw = L.nres[lane];
+    }
+    const int distinct = readlane(row_sum(__popcll(rw)), 0);          // words live in row 0
+    const int mpop = __popcll(rw & nw);
+    const int mincl = row_incl_scan(mpop);
+    const int total = readlane(mincl, NWORD - 1);
+    if (lane < NWORD) L.mpre[lane] = mincl - mpop;
+    const bool ins_ok = distinct <= max_distinct;
+    const int nins = ins_ok ? (total < max_inserts ? total : max_inserts) : 0;
+    const int nact = wave0_dispatch(L, S, nins, ins_ok, st, slot_stamp, se, sst);
+    if (lane == 0) {
+      L.misc[0] = nact;
+      L.misc[1] = nins;
+    }
+  }
+  lds_barrier();  // 3
+
+  const int nact = L.misc[0];
+  const int nins = L.misc[1];
+
+  // ---- expert side: routed flags, miss list, installs, post-update bucket counts ----------
+#pragma unroll
+  for (int j = 0; j < EJ; ++j) {
+    const int e = t + NT * j;
+    if (e >= E) continue;
+    const bool r = bit_of(L.rbits, e);
+    routed[e] = r ? 1 : 0;
+    const bool ismiss = r && tab[j] < 0;
+    int post = tab[j];
+    if (ismiss && nins > 0) {
+      const uint64_t mw = L.rbits[e >> 6] & L.nres[e >> 6];
+      const int rank = L.mpre[e >> 6] + __popcll(mw & ((1ull << (e & 63)) - 1ull));
+      if (rank < nins) miss[2 * rank] = e;
+      if (rank < nact) {
+        const int sl = L.vslot[rank];
+        const int old = L.vold[rank];
+        if (old >= 0 && old < E) {
+          table[old] = -1;
+          map_cold[old] = old;
+        }
+        table[e] = sl;
+        map_cold[e] = -1;
+        slot_expert[sl] = e;
+        slot_stamp[sl] = st;
+        miss[2 * rank + 1] = sl;
+        post = sl;
+      }
+    }
+    if (ALIGN) {
+      int c = 0;
+      if (r) {
+        if (staged) {
+#pragma unroll
+          for (int x = 0; x < TW; ++x) c += __popcll(L.tk.tmask[e][x]);
+        } else {
+          c = L.ecnt[e];
+        }
+      }
+      const bool hot = r && (unsigned)post < (unsigned)S;
+      if (hot) {
+        L.cnt_h[post] = c;
+        L.hexp[post] = e;
+      }
+      L.cnt_c[e] = (r && !hot) ? c : 0;
+      L.ecnt[e] = 0;  // general path: becomes the running per-expert base of the chunks
+    }
+  }
+  if (t == 0) {
+    step[0] = st;
+    n_miss[0] = nact;
+  }
+  if (!ALIGN) return;
+
+  lds_barrier();  // 4
+
+  // ---- block-padded exclusive scans: thread t owns a contiguous run of slots and experts ---
+  const Blk B(bs);
+  const int Ch = (S + NT - 1) / NT, Ce = (E + NT - 1) / NT;
+  const int h0 = t * Ch, h1 = min(h0 + Ch, S);
+  const int c0 = t * Ce, c1 = min(c0 + Ce, E);
+  int ph[EJ], pc[EJ], a = 0, b = 0;
+#pragma unroll
+  for (int j = 0; j < EJ; ++j) {
+    ph[j] = (j < Ch && h0 + j < h1) ? L.cnt_h[h0 + j] : 0;
+    pc[j] = (j < Ce && c0 + j < c1) ? L.cnt_c[c0 + j] : 0;
+    a += B.pad(ph[j]);
+    b += B.pad(pc[j]);
+  }
+  const int ai = wave_incl_scan(a), bi = wave_incl_scan(b);
+  if (lane == WAVE - 1) {
+    L.wsum[w][0] = ai;
+    L.wsum[w][1] = bi;
+  }
+  lds_barrier();  // 5
+  int runa = ai - a, runb = bi - b, tota = 0, totb = 0;
+#pragma unroll
+  for (int x = 0; x < NW; ++x) {
+    const int ya = L.wsum[x][0], yb = L.wsum[x][1];
+    if (x < w) {
+      runa += ya;
+      runb += yb;
+    }
+    tota += ya;
+    totb += yb;
+  }
+  if (t == 0) {
+    npad_hot[0] = tota;
+    npad_cold[0] = totb;
+  }
+  // bucket starts, expert ids, and (staged) the tokens of each bucket in index order
+  if (staged)
+    place_buckets(L, L.stage_h, L.stage_c, L.stage_eh, L.stage_ec, ph, pc, h0, h1, c0, c1, runa,
+                  runb, NB, B, true);
+  else
+    place_buckets(L, sorted_hot, sorted_cold, eids_hot, eids_cold, ph, pc, h0, h1, c0, c1, runa,
+                  runb, NB, B, false);
+  lds_barrier();  // 6
+
+  if (staged) {
+    // ---- copy the staged outputs out, coalesced --------------------------------------------
+    for (int k = t; k < Lsz; k += NT) {
+      sorted_hot[k] = L.stage_h[k];
+      sorted_cold[k] = L.stage_c[k];
+    }
+    for (int k = t; k < NB; k += NT) {
+      eids_hot[k] = L.stage_eh[k];
+      eids_cold[k] = L.stage_ec[k];
+    }
+    return;
+  }
+
+  // ---- general placement, chunk by chunk of NT tokens in index order ---------------------
+  for (int c = 0; c * NT < mk; ++c) {
+    const int i = c * NT + t;
+    int e = tok0;
+    bool v = v0;
+    if (c > 0) {
+      lds_barrier();
+      // fold the previous chunk's per-wave counts into the per-expert base, then rank this one
+#pragma unroll
+      for (int j = 0; j < EJ; ++j) {
+        const int x = t + NT * j;
+        if (x < E) {
+          int add = 0;
+#pragma unroll
+          for (int ww = 0; ww < NW; ++ww) {
+            add += L.tk.wcnt[ww][x];
+            L.tk.wcnt[ww][x] = 0;
+          }
+          L.ecnt[x] += add;
+        }
+      }
+      e = i < mk ? ids[i] : -1;
+      v = e >= 0 && e < E;
+      lds_barrier();
+      const uint64_t m = match_any(e, v, kbits);
+      inrank = mbcnt(m);
+      if (v && inrank == 0) L.tk.wcnt[w][e] = (uint8_t)__popcll(m);
+      lds_barrier();
+    }
+    if (v) {
+      int rank = L.ecnt[e] + inrank;
+      for (int ww = 0; ww < w; ++ww) rank += L.tk.wcnt[ww][e];
+      // post-update bucket of e: resident on entry, inserted now, or cold
+      int s = L.tab[e];
+      if ((unsigned)s >= (unsigned)S) {
+        s = -1;
+        if (nact > 0) {
+          const uint64_t mw = L.rbits[e >> 6] & L.nres[e >> 6];
+          if ((mw >> (e & 63)) & 1ull) {
+            const int mr = L.mpre[e >> 6] + __popcll(mw & ((1ull << (e & 63)) - 1ull));
+            if (mr < nact) s = L.vslot[mr];
+          }
+        }
+      }
+      if (s >= 0) {
+        const int pos = L.cum_h[s] + rank;
+        if (pos < Lsz) sorted_hot[pos] = i;
+      } else {
+        const int pos = L.cum_c[e] + rank;
+        if (pos < Lsz) sorted_cold[pos] = i;
+      }
+    }
+  }
+}
+
+// grid = (chunks, lanes), block = 256: block (c, j) copies misses j, j + lanes, ... ; within
+// a slab, 16-byte vectors are spread over the `chunks` blocks, four loads in flight per lane.
+// Destinations are written non-temporally: a gathered slab is read by the next GEMM once.
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(NT) void gather_k(v4u* d0, const v4u* s0, long v0,
+                                               v4u* d1, const v4u* s1, long v1,
+                                               v4u* d2, const v4u* s2, long v2,
+                                               v4u* d3, const v4u* s3, long v3,
+                                               v4u* d4, const v4u* s4, long v4,
+                                               v4u* d5, const v4u* s5, long v5,
+                                               const int* __restrict__ miss,
+                                               const int* __restrict__ n_miss) {
+  const int nm = n_miss[0];
+  const long stride = (long)gridDim.x * NT;
+  const long start = (long)blockIdx.x * NT + threadIdx.x;
+  for (int j = blockIdx.y; j < nm; j += gridDim.y) {
+    const long e = miss[2 * j], sl = miss[2 * j + 1];
+    v4u* dd[6] = {d0, d1, d2, d3, d4, d5};
+    const v4u* ss[6] = {s0, s1, s2, s3, s4, s5};
+    const long vv[6] = {v0, v1, v2, v3, v4, v5};
+#pragma unroll
+    for (int b = 0; b < 6; ++b) {
+      const v4u* __restrict__ p = ss[b] + e * vv[b];
+      v4u* __restrict__ q = dd[b] + sl * vv[b];
+      const long V = vv[b];
+      long i = start;
+      for (; i + 3 * stride < V; i += 4 * stride) {
+        const v4u x0 = p[i], x1 = p[i + stride], x2 = p[i + 2 * stride], x3 = p[i + 3 * stride];
+        __builtin_nontemporal_store(x0, q + i);
+        __builtin_nontemporal_store(x1, q + i + stride);
+        __builtin_nontemporal_store(x2, q + i + 2 * stride);
+        __builtin_nontemporal_store(x3, q + i + 3 * stride);
+      }
+      for (; i < V; i += stride) __builtin_nontemporal_store(p[i], q + i);
+    }
+  }
+}
+
+}  // namespace rlu
+
+extern "C" {
+
+// kernels/lru/r4d_lru.hip:579-589
+int r4d_lru_manage(const int* topk_ids, int mk, int E, int S, int max_distinct,
+                   int max_inserts, int* table, int* map_cold, int* slot_expert,
+                   long long* slot_stamp, unsigned char* routed, long long* step, int* miss,
+                   int* n_miss, hipStream_t stream) {
+  if (E <= 0 || E > rlu::MAXE || S <= 0 || S > rlu::MAXS) return -1;
+  if (max_inserts < 0 || max_inserts > rlu::MAXINS || mk < 0) return -1;
+  hipLaunchKernelGGL(rlu::lru_k<false>, dim3(1), dim3(rlu::NT), 0, stream, topk_ids, mk, E, S,
+                     max_distinct, max_inserts, table, map_cold, slot_expert, slot_stamp,
+                     routed, step, miss, n_miss, 1, 0, 0, nullptr, nullptr, nullptr, nullptr,
+                     nullptr, nullptr);
+  return (int)hipGetLastError();
+}
+
+// kernels/lru/r4d_lru.hip:596-610
+int r4d_lru_fused(const int* topk_ids, int mk, int E, int S, int max_distinct,
+                  int max_inserts, int* table, int* map_cold, int* slot_expert,
+                  long long* slot_stamp, unsigned char* routed, long long* step, int* miss,
+                  int* n_miss, int bs, int L, int NB, int* sorted_hot, int* eids_hot,
+                  int* npad_hot, int* sorted_cold, int* eids_cold, int* npad_cold,
+                  hipStream_t stream) {
+  if (E <= 0 || E > rlu::MAXE || S <= 0 || S > rlu::MAXS) return -1;
+  if (bs <= 0 || L <= 0 || NB <= 0 || mk < 0) return -1;
+  if (max_inserts < 0 || max_inserts > rlu::MAXINS) return -1;
+  hipLaunchKernelGGL(rlu::lru_k<true>, dim3(1), dim3(rlu::NT), 0, stream, topk_ids, mk, E, S,
+                     max_distinct, max_inserts, table, map_cold, slot_expert, slot_stamp,
+                     routed, step, miss, n_miss, bs, L, NB, sorted_hot, eids_hot, npad_hot,
+                     sorted_cold, eids_cold, npad_cold);
+  return (int)hipGetLastError();
+}
+
+// kernels/lru/r4d_lru.hip:612-629
+int r4d_lru_gather(void* d0, const void* s0, long b0, void* d1, const void* s1, long b1,
+                   void* d2, const void* s2, long b2, void* d3, const void* s3, long b3,
+                   void* d4, const void* s4, long b4, void* d5, const void* s5, long b5,
+                   const int* miss, const int* n_miss, int chunks, int lanes,
+                   hipStream_t stream) {
+  const long bs[6] = {b0, b1, b2, b3, b4, b5};
+  for (int i = 0; i < 6; i++)
+    if (bs[i] <= 0 || bs[i] % 16) return -1;
+  if (chunks <= 0 || lanes <= 0) return -1;
+  hipLaunchKernelGGL(rlu::gather_k, dim3(chunks, lanes), dim3(rlu::NT), 0, stream,
+                     (rlu::v4u*)d0, (const rlu::v4u*)s0, b0 / 16, (rlu::v4u*)d1,
+                     (const rlu::v4u*)s1, b1 / 16, (rlu::v4u*)d2, (const rlu::v4u*)s2, b2 / 16,
+                     (rlu::v4u*)d3, (const rlu::v4u*)s3, b3 / 16, (rlu::v4u*)d4,
+                     (const rlu::v4u*)s4, b4 / 16, (rlu::v4u*)d5, (const rlu::v4u*)s5, b5 / 16,
+                     miss, n_miss);
+  return (int)hipGetLastError();
+}
+
+}  // extern "C"

@@ -1,0 +1,339 @@
+"""GPU parity of the device LRU (r4d_lru_manage / r4d_lru_fused / r4d_lru_gather) through the
+C-ABI, against the numpy oracle and against the reference's own kernel compiled from
+/root/reference by oracle/Makefile (oracle/_ref/librlu_ref.so, when present).
+
+Mirrors tests/lru/test_lru.py (policy suites + gather byte identity), tests/lru/test_fused.py
+(fused vs manager + align, edges, HIP-graph replay, negative control) and
+tests/lru/test_victim_equiv.py (19 victim cases), all bit-exact.
+"""
+from __future__ import annotations
+
+import ctypes
+import pathlib
+
+import numpy as np
+import pytest
+
+from conftest import gpu_case
+from lru_cases import POLICY_SUITES, VICTIM_CASES, c1_trace, policy_start, victim_case
+from oracle import lru as olru
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+BS = 16
+REF_SO = pathlib.Path(__file__).resolve().parent.parent / "oracle" / "_ref" / "librlu_ref.so"
+NAMES = olru.LruState.NAMES
+
+
+def to_dev(s: olru.LruState) -> dict:
+    return {n: torch.from_numpy(np.ascontiguousarray(getattr(s, n))).to(DEV) for n in NAMES}
+
+
+def from_dev(d: dict, like: olru.LruState) -> olru.LruState:
+    out = like.copy()
+    for n in NAMES:
+        getattr(out, n)[...] = d[n].cpu().numpy()
+    return out
+
+
+def assert_state(got: dict, want: olru.LruState, tag: str, skip=("routed",)):
+    for n in NAMES:
+        if n in skip:
+            continue
+        g = got[n].cpu().numpy()
+        w = getattr(want, n)
+        assert np.array_equal(g, w), f"{tag}: '{n}' differs in {int((g != w).sum())} entries"
+
+
+def call(libh, fn, ids_t, d, md, mi, out=None, bs=BS):
+    args = [ctypes.c_void_p(d[n].data_ptr()) for n in NAMES]
+    E, S = d["table"].numel(), d["slot_expert"].numel()
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    if fn == "manage":
+        rc = libh.r4d_lru_manage(ctypes.c_void_p(ids_t.data_ptr()), ids_t.numel(), E, S, md, mi,
+                                 *args, st)
+    else:
+        rc = libh.r4d_lru_fused(ctypes.c_void_p(ids_t.data_ptr()), ids_t.numel(), E, S, md, mi,
+                                *args, bs, out[0].numel(), out[1].numel(),
+                                *[ctypes.c_void_p(o.data_ptr()) for o in out], st)
+    assert rc == 0, f"{fn} rc={rc}"
+
+
+def new_out(mk, E, bs=BS, fill=None):
+    L, NB = olru.align_sizes(mk, E, bs)
+    mk_ = lambda n: (torch.empty(n, dtype=torch.int32, device=DEV) if fill is None
+                     else torch.full((n,), fill, dtype=torch.int32, device=DEV))
+    return [mk_(L), mk_(NB), mk_(1), mk_(L), mk_(NB), mk_(1)]
+
+
+@pytest.fixture(scope="module")
+def mine(pkg):
+    return pkg.lib()
+
+
+@pytest.fixture(scope="module")
+def ref():
+    if not REF_SO.exists():
+        pytest.skip("reference library not built (oracle/Makefile ref needs /root/reference)")
+    h = ctypes.CDLL(str(REF_SO))
+    P, I = ctypes.c_void_p, ctypes.c_int
+    h.r4d_lru_manage.restype = I
+    h.r4d_lru_manage.argtypes = [P] + [I] * 5 + [P] * 9
+    h.r4d_lru_fused.restype = I
+    h.r4d_lru_fused.argtypes = [P] + [I] * 5 + [P] * 8 + [I] * 3 + [P] * 7
+    return h
+
+
+@pytest.mark.parametrize("suite", POLICY_SUITES, ids=[s[0] for s in POLICY_SUITES])
+def test_policy_manage_vs_oracle(mine, suite):
+    """tests/lru/test_lru.py:148-169: every field after every step."""
+    name, E, S, gen, nsteps, md, mi = suite
+    rng, s = policy_start(E, S, maxi=mi)
+    d = to_dev(s)
+    for n in range(nsteps):
+        ids = gen(rng, n).ravel().astype(np.int32)
+        olru.manage(s, ids, md, mi)
+        gpu_case(f"policy {name} step {n} E={E} S={S} mk={ids.size}") if n == 0 else None
+        call(mine, "manage", torch.from_numpy(ids).to(DEV), d, md, mi)
+        torch.cuda.synchronize()
+        assert_state(d, s, f"{name} step {n}", skip=())
+        assert not olru.check_invariants(s)
+
+
+def test_c1_fused_vs_oracle_and_golden(mine):
+    """The 64-step LRU workload (E=512, S=257, top-10, 5 rows): state and both align outputs
+    bit-exact against the oracle after every step, and against the committed fixture."""
+    ids_all, s = c1_trace()
+    gold = np.load(pathlib.Path(__file__).parent / "golden" / "lru_c1.npz")
+    d = to_dev(s)
+    mk = ids_all.shape[1]
+    for n in range(ids_all.shape[0]):
+        want = olru.fused(s, ids_all[n], BS)
+        out = new_out(mk, 512, fill=-12345)
+        gpu_case(f"c1 fused step {n}") if n == 0 else None
+        call(mine, "fused", torch.from_numpy(ids_all[n]).to(DEV), d, s.max_distinct,
+             s.max_inserts, out)
+        torch.cuda.synchronize()
+        assert_state(d, s, f"c1 step {n}", skip=())
+        for i, (g, w) in enumerate(zip(out, want)):
+            assert np.array_equal(g.cpu().numpy(), w), f"c1 step {n}: align output {i}"
+        for i, name in enumerate(("sorted_hot", "eids_hot", "npad_hot", "sorted_cold",
+                                  "eids_cold", "npad_cold")):
+            assert np.array_equal(out[i].cpu().numpy(), gold[f"{name}_{n}"]), (n, name)
+        for name in NAMES:
+            assert np.array_equal(d[name].cpu().numpy(), gold[f"{name}_{n}"]), (n, name)
+
+
+@pytest.mark.parametrize("case", VICTIM_CASES, ids=[c[0] for c in VICTIM_CASES])
+@pytest.mark.parametrize("fn", ["manage", "fused"])
+def test_victim_cases_vs_oracle(mine, case, fn):
+    """tests/lru/test_victim_equiv.py:137-182 against the oracle (full state, all outputs)."""
+    name, kw = case
+    ids, s = victim_case(**kw)
+    d = to_dev(s)
+    gpu_case(f"victim {name} {fn} E={s.E} S={s.S} mk={ids.size} maxi={kw['maxi']}")
+    out = new_out(ids.size, s.E, fill=-12345) if fn == "fused" else None
+    call(mine, fn, torch.from_numpy(ids).to(DEV), d, s.max_distinct, s.max_inserts, out)
+    torch.cuda.synchronize()
+    want = olru.fused(s, ids, BS) if fn == "fused" else olru.manage(s, ids)
+    assert_state(d, s, name, skip=())
+    if fn == "fused":
+        for i, (g, w) in enumerate(zip(out, want)):
+            assert np.array_equal(g.cpu().numpy(), w), f"{name}: align output {i}"
+
+
+def _cmp_align_multiset(g, r, mk, bs=BS):
+    """tests/lru/test_fused.py:133-173: npad and expert_ids exact, sorted_ids as a multiset per
+    bucket, sentinel past npad."""
+    gs, ge, gn = [x.cpu().numpy() for x in g]
+    rs, re_, rn = [x.cpu().numpy() for x in r]
+    assert gn[0] == rn[0]
+    assert np.array_equal(ge, re_)
+    n = int(gn[0])
+    by = lambda s_, e_: {int(k): sorted(s_[:n][np.repeat(e_[:n // bs], bs) == k].tolist())
+                         for k in np.unique(e_[:n // bs])}
+    assert by(gs, ge) == by(rs, re_)
+    assert (gs[n:] == mk).all() and (rs[n:] == mk).all()
+
+
+@pytest.mark.parametrize("case", VICTIM_CASES, ids=[c[0] for c in VICTIM_CASES])
+def test_victim_cases_vs_reference_kernel(mine, ref, case):
+    """Same pristine state through this library and through the reference kernel compiled
+    from kernels/lru/r4d_lru.hip: the whole state bit-exact; align exact when mk <= 256 (the
+    reference's deterministic path), per-bucket multiset above (its atomic cursors)."""
+    name, kw = case
+    ids, s = victim_case(**kw)
+    ids_t = torch.from_numpy(ids).to(DEV)
+    for fn in ("manage", "fused"):
+        a, b = to_dev(s), to_dev(s)
+        oa = new_out(ids.size, s.E, fill=-12345) if fn == "fused" else None
+        ob = new_out(ids.size, s.E, fill=-12345) if fn == "fused" else None
+        gpu_case(f"vs-ref {name} {fn}")
+        call(mine, fn, ids_t, a, s.max_distinct, s.max_inserts, oa)
+        call(ref, fn, ids_t, b, s.max_distinct, s.max_inserts, ob)
+        torch.cuda.synchronize()
+        for n in NAMES:
+            assert torch.equal(a[n], b[n]), f"{name}/{fn}: '{n}' differs from the reference"
+        if fn == "fused":
+            if ids.size <= 256:
+                for i in range(6):
+                    assert torch.equal(oa[i], ob[i]), f"{name}: align output {i}"
+            else:
+                _cmp_align_multiset(oa[0:3], ob[0:3], ids.size)
+                _cmp_align_multiset(oa[3:6], ob[3:6], ids.size)
+
+
+def test_c1_trace_vs_reference_kernel(mine, ref):
+    """The 64-step trace through both kernels, side by side: identical state every step."""
+    ids_all, s = c1_trace()
+    a, b = to_dev(s), to_dev(s)
+    for n in range(ids_all.shape[0]):
+        ids_t = torch.from_numpy(ids_all[n]).to(DEV)
+        oa, ob = new_out(50, 512), new_out(50, 512)
+        call(mine, "fused", ids_t, a, s.max_distinct, s.max_inserts, oa)
+        call(ref, "fused", ids_t, b, s.max_distinct, s.max_inserts, ob)
+        torch.cuda.synchronize()
+        for nm in NAMES:
+            assert torch.equal(a[nm], b[nm]), f"step {n}: '{nm}'"
+        for i in range(6):
+            assert torch.equal(oa[i], ob[i]), f"step {n}: align output {i}"
+
+
+@pytest.mark.parametrize("rows", [1, 4, 20, 40, 205])
+def test_fused_geometries(mine, rows):
+    """tests/lru/test_fused.py:265-280: mk = 10 .. 2050 incl. the chunked placement path."""
+    E, S = 512, 257
+    rng = np.random.default_rng(7)
+    from oracle import trace as otrace
+    p = otrace.zipf_p(E, 1.1)
+    _, s = victim_case(E=E, S=S, mk=10, k_cold=0, maxi=64, seed=3)
+    s.max_distinct = max(1, int(S * 0.5))
+    d = to_dev(s)
+    for n in range(6):
+        ids = np.concatenate([rng.choice(E, 10, replace=False, p=p)
+                              for _ in range(rows)]).astype(np.int32)
+        want = olru.fused(s, ids, BS)
+        out = new_out(ids.size, E, fill=-12345)
+        gpu_case(f"geometry rows={rows} step {n}") if n == 0 else None
+        call(mine, "fused", torch.from_numpy(ids).to(DEV), d, s.max_distinct, s.max_inserts,
+             out)
+        torch.cuda.synchronize()
+        assert_state(d, s, f"rows={rows} step {n}", skip=())
+        for i, (g, w) in enumerate(zip(out, want)):
+            assert np.array_equal(g.cpu().numpy(), w), f"rows={rows} step {n}: output {i}"
+        # hot + cold partition [0, mk) (tests/lru/test_fused.py:186-195)
+        hot = out[0].cpu().numpy()[:int(out[2].item())]
+        cold = out[3].cpu().numpy()[:int(out[5].item())]
+        tok = np.sort(np.concatenate([hot[hot != ids.size], cold[cold != ids.size]]))
+        assert np.array_equal(tok, np.arange(ids.size))
+
+
+def test_fused_edges(mine):
+    """tests/lru/test_fused.py:282-293: forced read-through and a zero-miss replay."""
+    ids_all, s = c1_trace()
+    d = to_dev(s)
+    for md, tag in ((0, "read-through"), (s.max_distinct, "warm"), (s.max_distinct, "zero-miss")):
+        out = new_out(50, 512, fill=-12345)
+        want = olru.fused(s, ids_all[0], BS, max_distinct=md)
+        gpu_case(f"edge {tag}")
+        call(mine, "fused", torch.from_numpy(ids_all[0]).to(DEV), d, md, s.max_inserts, out)
+        torch.cuda.synchronize()
+        assert_state(d, s, tag, skip=())
+        for i, (g, w) in enumerate(zip(out, want)):
+            assert np.array_equal(g.cpu().numpy(), w), f"{tag}: output {i}"
+        if tag == "zero-miss":
+            assert int(d["n_miss"].item()) == 0
+
+
+def test_fused_graph_replay(mine):
+    """tests/lru/test_fused.py:295-364: 12 replays of a captured call with changing routing
+    equal 12 eager calls, state and outputs; a zero-insert step after an inserting one leaves
+    no stale output."""
+    ids_all, s0 = c1_trace()
+    mk = ids_all.shape[1]
+    ids_static = torch.zeros(mk, dtype=torch.int32, device=DEV)
+    out = new_out(mk, 512)
+    d = to_dev(s0)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        ids_static.copy_(torch.from_numpy(ids_all[0]))
+        call(mine, "fused", ids_static, d, s0.max_distinct, s0.max_inserts, out)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    gpu_case("graph capture of r4d_lru_fused")
+    with torch.cuda.graph(g):
+        call(mine, "fused", ids_static, d, s0.max_distinct, s0.max_inserts, out)
+    torch.cuda.synchronize()
+    fresh = to_dev(s0)
+    for n in NAMES:
+        d[n].copy_(fresh[n])
+    s = s0.copy()
+    seq = list(range(12)) + [11]          # the last replay repeats routing: zero inserts
+    for k, n in enumerate(seq):
+        ids_static.copy_(torch.from_numpy(ids_all[n]))
+        g.replay()
+        torch.cuda.synchronize()
+        want = olru.fused(s, ids_all[n], BS)
+        assert_state(d, s, f"replay {k}", skip=())
+        for i, (gg, w) in enumerate(zip(out, want)):
+            assert np.array_equal(gg.cpu().numpy(), w), f"replay {k}: output {i}"
+    assert int(d["n_miss"].item()) == 0
+
+
+def _uva(nbytes):
+    t = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
+    hip = ctypes.CDLL("libamdhip64.so")
+    dp = ctypes.c_void_p()
+    rc = hip.hipHostGetDevicePointer(ctypes.byref(dp), ctypes.c_void_p(t.data_ptr()),
+                                     ctypes.c_uint(0))
+    assert rc == 0, f"hipHostGetDevicePointer rc={rc}"
+    return t, dp.value
+
+
+def test_gather_bytes_from_pinned_host(pkg):
+    """tests/lru/test_lru.py:210-258: 40 steps of manage + gather from pinned host memory;
+    every inserted slab of all six buffers byte-equal to its source."""
+    E, S = 512, 257
+    sizes = [3932160 // 16, 1966080 // 16, 960, 480, 960, 480]   # fp8 layer, scaled down
+    g = torch.Generator().manual_seed(1)
+    src_h, src_d, dst = [], [], []
+    for b in sizes:
+        h, dp = _uva(E * b)
+        h.copy_(torch.randint(0, 256, (E * b,), dtype=torch.uint8, generator=g))
+        src_h.append(h)
+        src_d.append(dp)
+        dst.append(torch.zeros(S * b, dtype=torch.uint8, device=DEV))
+    _, s = victim_case(E=E, S=S, mk=50, k_cold=0, maxi=64, seed=3)
+    s.max_distinct = 128
+    d = to_dev(s)
+    rng = np.random.default_rng(11)
+    views_d = [x.view(S, b) for x, b in zip(dst, sizes)]
+    views_s = [x.view(E, b) for x, b in zip(src_h, sizes)]
+    for n in range(40):
+        ids = np.concatenate([rng.choice(E, 10, replace=False) for _ in range(5)]).astype(np.int32)
+        olru.manage(s, ids)
+        gpu_case(f"gather step {n}") if n == 0 else None
+        call(pkg.lib(), "manage", torch.from_numpy(ids).to(DEV), d, s.max_distinct,
+             s.max_inserts)
+        pkg._r4d_lru_gather(views_d, views_s, d["miss"], d["n_miss"], 8, 16, src_ptrs=src_d)
+        torch.cuda.synchronize()
+        assert_state(d, s, f"gather step {n}", skip=())
+        nm = int(s.n_miss[0])
+        for e, sl in s.miss[:nm].tolist():
+            for i in range(6):
+                assert torch.equal(views_d[i][sl].cpu(), views_s[i][e]), (n, e, sl, i)
+
+
+def test_gather_rejects_bad_sizes(pkg):
+    d = torch.zeros(64, dtype=torch.uint8, device=DEV).view(4, 16)
+    bad = torch.zeros(4, 8, dtype=torch.uint8, device=DEV)
+    m = torch.zeros(4, 2, dtype=torch.int32, device=DEV)
+    nm = torch.zeros(1, dtype=torch.int32, device=DEV)
+    with pytest.raises(RuntimeError):
+        pkg._r4d_lru_gather([bad] * 6, [bad] * 6, m, nm, 8, 16)
+    with pytest.raises(RuntimeError):
+        pkg._r4d_lru_gather([d] * 6, [d] * 6, m, nm, 0, 16)
