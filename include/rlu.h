@@ -57,6 +57,57 @@ int r4d_lru_gather(void* d0, const void* s0, long b0, void* d1, const void* s1, 
                    const int* miss, const int* n_miss, int chunks, int lanes,
                    hipStream_t stream);
 
+/* ---- activation quant, SiLU-mul-quant, top-k reduction ----------------------------------
+ * bf16 activations (uint16 bit patterns), e4m3fn outputs (one byte each), float32 scales.
+ * group = 128: one scale per 128 columns (per-token-group-128, the GEMM input format of this
+ * path); group = 0: one scale per row (the reference's per-token form). Scale rule for both:
+ * max(amax / 448, 1 / (448 * 512)); q = e4m3(clamp(x / scale, +-448)), nearest-even.
+ * Returns -1 on bad sizes (K or d not a multiple of 8, ld too small), -2 on a bad group,
+ * -3 when a per-row (group 0) row is too long for one workgroup.
+ */
+
+/* Replaces the activation quant of patches/.../mxfp4/r4dhip.py.diff:22-34 (fp8_quant_shared
+ * -> vLLM scaled_fp8_quant) and kernels/fp8_target_lmhead.py:72-73 (vLLM
+ * per_token_group_quant_fp8). x [rows, K] with row stride ldx (elements); q [rows, K];
+ * scale [rows, K/128] or [rows]. */
+int rlu_quant_fp8_group(const void* x, int rows, int K, int ldx, int group, void* q,
+                        float* scale, hipStream_t stream);
+
+/* Replaces kernels/fused_silu_mul_quant.py:75-101 (silu_mul_quant): x [rows, 2d] bf16 = gate |
+ * up with row stride ldx; act = bf16(bf16(silu(g)) * u) is written to `act` [rows, d] when it
+ * is not null; q [rows, d]; scale [rows, d/128] or [rows]. */
+int rlu_silu_mul_quant(const void* x, int rows, int d, int ldx, int group, void* q,
+                       float* scale, void* act, hipStream_t stream);
+
+/* Replaces vLLM's ops.moe_sum as called at patches/.../r4d_mxfp4_moe.py.lru.diff:696:
+ * out[m, :] = bf16(sum_k in[m * top_k + k, :]) with float32 accumulation in k order.
+ * H % 8 == 0. */
+int rlu_moe_sum(const void* in, int M, int top_k, int H, void* out, hipStream_t stream);
+
+/* ---- fp8 block-scaled GEMMs on MFMA ----------------------------------------------------------
+ * Replaces the closed r4d_gemm_moe_mxfp4a8_nt_b16 behind the op r4d_mxfp4_moe_gemm_into
+ * (patches/.../r4d_mxfp4_moe.py.lru.diff:363-395; argument order of
+ * tests/k1/moe_ref_harness.py:55-56,221-226), for e4m3 weights with 128x128 float32 block scales:
+ *   qx [mtk/top_k, K] e4m3, xs [mtk/top_k, K/128] f32, wq [E, N, K] e4m3, ws [E, N/128, K/128]
+ *   f32, wref unused (the reference's second scale slot), y [mtk, N] bf16, sorted_ids [em],
+ *   expert_ids [em/16], num_post_pad [1] (read on the device), topk_weights [mtk] f32 or null.
+ * Row contract of the reference kernel: sorted ids >= mtk are padding, expert id -1 skips the
+ * block, only named rows are written, y[row] *= topk_weights[row] when given.
+ * wv = workgroups per CU of the persistent grid (0: 4), sk = split-K (must be 1), npw =
+ * 16-column tiles per wave (1, 2, 4, 8). Returns -1 bad sizes, -2 K or N not a multiple of
+ * 128, -4 sk != 1, -5 bad wv, -6 bad npw; the closed launcher aborted instead. */
+int r4d_gemm_moe_fp8blk_nt_b16(const void* qx, const float* xs, const void* wq,
+                               const float* ws, const void* wref, void* y,
+                               const int* sorted_ids, const int* expert_ids,
+                               const int* num_post_pad, const float* topk_weights, int em,
+                               int mtk, int top_k, int K, int N, int wv, int sk, int npw,
+                               hipStream_t stream);
+
+/* Replaces fp8hip_gemm_w8a8_launch behind gemm_fp8_block (kernels/fp8_target_lmhead.py:70-74):
+ * y [M, N] bf16 = qx [M, K] (xs [M, K/128]) x w [N, K] (ws [N/128, K/128])^T, 1 <= M <= 16. */
+int rlu_gemm_fp8blk_m16(const void* qx, const float* xs, const void* w, const float* ws,
+                        void* y, int M, int N, int K, int wv, int npw, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

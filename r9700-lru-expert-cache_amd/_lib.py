@@ -22,6 +22,11 @@ SIGNATURES: dict[str, tuple] = {
     "r4d_lru_manage": (_I, [_P] + [_I] * 5 + [_P] * 9),
     "r4d_lru_fused": (_I, [_P] + [_I] * 5 + [_P] * 8 + [_I] * 3 + [_P] * 7),
     "r4d_lru_gather": (_I, [_P, _P, _L] * 6 + [_P, _P, _I, _I, _P]),
+    "rlu_quant_fp8_group": (_I, [_P, _I, _I, _I, _I, _P, _P, _P]),
+    "rlu_silu_mul_quant": (_I, [_P, _I, _I, _I, _I, _P, _P, _P, _P]),
+    "rlu_moe_sum": (_I, [_P, _I, _I, _I, _P, _P]),
+    "r4d_gemm_moe_fp8blk_nt_b16": (_I, [_P] * 10 + [_I] * 8 + [_P]),
+    "rlu_gemm_fp8blk_m16": (_I, [_P] * 5 + [_I] * 5 + [_P]),
 }
 
 

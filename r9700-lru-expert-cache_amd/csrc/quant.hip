@@ -1,0 +1,239 @@
+// Activation quantizers and the top-k reduction of the MoE decode path, for gfx950.
+//
+//   group_quant_k     per-token-group-128 (or per-token) e4m3 quant of bf16 activations --
+//                     the GEMM1 input (patches/.../mxfp4/r4dhip.py.diff:22-34 does it per token
+//                     with vLLM's scaled_fp8_quant; this path uses 128-column groups).
+//   silu_mul_quant_k  silu(gate) * up + the same quant, one pass (kernels/fused_silu_mul_quant.py
+//                     :26-57): silu rounded to bf16 before the multiply, the product rounded to
+//                     bf16, amax over the rounded product, scale = max(amax / 448, 1/(448*512)),
+//                     q = e4m3(clamp(a / scale, +-448)) with a true division.
+//   moe_sum_k         out[m] = sum_k in[m * top_k + k] (vLLM's moe_sum, called at
+//                     patches/.../r4d_mxfp4_moe.py.lru.diff:696), float32 accumulation in k order.
+//
+// Layout: one workgroup per row; each lane owns 8 consecutive columns, so a 16-lane DPP row
+// covers exactly one 128-column group and the group amax is a 4-step DPP reduction.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "numerics.h"
+#include "rlu.h"
+#include "wave.h"
+
+namespace rlu {
+
+constexpr int QT = 256;   // threads per row
+
+__device__ __forceinline__ uint32_t row_max_u32(uint32_t v) {
+  v = max(v, (uint32_t)dpp<0xb1>((int)v, (int)v));
+  v = max(v, (uint32_t)dpp<0x4e>((int)v, (int)v));
+  v = max(v, (uint32_t)dpp<0x141>((int)v, (int)v));
+  v = max(v, (uint32_t)dpp<0x140>((int)v, (int)v));
+  return v;
+}
+
+// |x| of non-negative floats compares like its bit pattern
+__device__ __forceinline__ uint32_t abs_bits(float x) { return __float_as_uint(x) & 0x7fffffffu; }
+
+__device__ __forceinline__ uint32_t block_max_u32(uint32_t v, uint32_t* sh) {
+  v = row_max_u32(v);
+  v = max(max((uint32_t)readlane((int)v, 0), (uint32_t)readlane((int)v, 16)),
+          max((uint32_t)readlane((int)v, 32), (uint32_t)readlane((int)v, 48)));
+  if (lane_id() == 0) sh[threadIdx.x / WAVE] = v;
+  lds_barrier();
+  uint32_t r = 0;
+  for (int i = 0; i < QT / WAVE; ++i) r = max(r, sh[i]);
+  return r;
+}
+
+__device__ __forceinline__ float scale_of(uint32_t amax_bits) {
+  const float s = __fdiv_rn(__uint_as_float(amax_bits), E4M3_MAX);
+  return s > MIN_SCALE ? s : MIN_SCALE;
+}
+
+// quantize 8 values with one scale -> 8 e4m3 bytes
+__device__ __forceinline__ uint2 quant8(const float (&a)[8], float s) {
+  uint32_t w[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float x0 = __fdiv_rn(a[2 * j], s), x1 = __fdiv_rn(a[2 * j + 1], s);
+    x0 = fminf(fmaxf(x0, -E4M3_MAX), E4M3_MAX);
+    x1 = fminf(fmaxf(x1, -E4M3_MAX), E4M3_MAX);
+    w[j] = f32x2_to_e4m3(x0, x1);
+  }
+  return make_uint2(w[0] | (w[1] << 16), w[2] | (w[3] << 16));
+}
+
+__device__ __forceinline__ void load8_bf16(const uint16_t* p, float (&v)[8]) {
+  const uint4 r = *reinterpret_cast<const uint4*>(p);
+  const uint32_t u[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    v[2 * j] = __uint_as_float(u[j] << 16);
+    v[2 * j + 1] = __uint_as_float(u[j] & 0xffff0000u);
+  }
+}
+
+// group == 128: one scale per 128 columns; group == 0: one scale per row. K % 8 == 0 and, for
+// group 128, K % 128 == 0 (checked by the entry point).
+__global__ __launch_bounds__(QT) void group_quant_k(const uint16_t* __restrict__ x, int K,
+                                                    int ldx, int group,
+                                                    uint8_t* __restrict__ q,
+                                                    float* __restrict__ scale) {
+  __shared__ uint32_t sh[QT / WAVE];
+  const int row = blockIdx.x;
+  const uint16_t* xr = x + (size_t)row * ldx;
+  uint8_t* qr = q + (size_t)row * K;
+  if (group == 0) {
+    uint32_t m = 0;
+    for (int c = threadIdx.x * 8; c < K; c += QT * 8) {
+      float v[8];
+      load8_bf16(xr + c, v);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) m = max(m, abs_bits(v[j]));
+    }
+    const float s = scale_of(block_max_u32(m, sh));
+    if (threadIdx.x == 0) scale[row] = s;
+    for (int c = threadIdx.x * 8; c < K; c += QT * 8) {
+      float v[8];
+      load8_bf16(xr + c, v);
+      *reinterpret_cast<uint2*>(qr + c) = quant8(v, s);
+    }
+    return;
+  }
+  const int ng = K / 128;
+  for (int base = 0; base < K; base += QT * 8) {     // uniform trip count over the block
+    const int c = base + threadIdx.x * 8;
+    const bool in = c < K;
+    float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (in) load8_bf16(xr + c, v);
+    uint32_t m = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) m = max(m, abs_bits(v[j]));
+    const float s = scale_of(row_max_u32(m));
+    if (in) {
+      *reinterpret_cast<uint2*>(qr + c) = quant8(v, s);
+      if ((threadIdx.x & 15) == 0) scale[(size_t)row * ng + c / 128] = s;
+    }
+  }
+}
+
+// x [rows, 2d] bf16 (gate | up), ldx elements apart; q [rows, d]; scale [rows, d/group or 1];
+// act [rows, d] bf16 or null.
+__global__ __launch_bounds__(QT) void silu_mul_quant_k(const uint16_t* __restrict__ x, int d,
+                                                       int ldx, int group,
+                                                       uint8_t* __restrict__ q,
+                                                       float* __restrict__ scale,
+                                                       uint16_t* __restrict__ act) {
+  __shared__ uint32_t sh[QT / WAVE];
+  const int row = blockIdx.x;
+  const uint16_t* g = x + (size_t)row * ldx;
+  const uint16_t* u = g + d;
+  uint8_t* qr = q + (size_t)row * d;
+  auto compute8 = [&](int c, float (&a)[8]) {
+    float gv[8], uv[8];
+    load8_bf16(g + c, gv);
+    load8_bf16(u + c, uv);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) a[j] = bf16_to_f32(f32_to_bf16(__fmul_rn(silu_bf16(gv[j]), uv[j])));
+    if (act) {
+      uint32_t w[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        w[j] = (uint32_t)f32_to_bf16(a[2 * j]) | ((uint32_t)f32_to_bf16(a[2 * j + 1]) << 16);
+      *reinterpret_cast<uint4*>(act + (size_t)row * d + c) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+  };
+  if (group == 0) {
+    // per-token: the row is held in registers between the amax and the quant (d <= QT*8*4)
+    float a[4][8];
+    uint32_t m = 0;
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int c = (it * QT + threadIdx.x) * 8;
+      if (c < d) {
+        compute8(c, a[it]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) m = max(m, abs_bits(a[it][j]));
+      }
+    }
+    const float s = scale_of(block_max_u32(m, sh));
+    if (threadIdx.x == 0) scale[row] = s;
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int c = (it * QT + threadIdx.x) * 8;
+      if (c < d) *reinterpret_cast<uint2*>(qr + c) = quant8(a[it], s);
+    }
+    return;
+  }
+  const int ng = d / 128;
+  for (int base = 0; base < d; base += QT * 8) {
+    const int c = base + threadIdx.x * 8;
+    const bool in = c < d;
+    float a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (in) compute8(c, a);
+    uint32_t m = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) m = max(m, abs_bits(a[j]));
+    const float s = scale_of(row_max_u32(m));
+    if (in) {
+      *reinterpret_cast<uint2*>(qr + c) = quant8(a, s);
+      if ((threadIdx.x & 15) == 0) scale[(size_t)row * ng + c / 128] = s;
+    }
+  }
+}
+
+// out [M, H] = sum over k of in [M * top_k + k, H]; grid (M, ceil(H / (QT*8)))
+__global__ __launch_bounds__(QT) void moe_sum_k(const uint16_t* __restrict__ in, int top_k,
+                                                int H, uint16_t* __restrict__ out) {
+  const int m = blockIdx.x;
+  const int c = (blockIdx.y * QT + threadIdx.x) * 8;
+  if (c >= H) return;
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int k = 0; k < top_k; ++k) {
+    float v[8];
+    load8_bf16(in + ((size_t)m * top_k + k) * H + c, v);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = __fadd_rn(acc[j], v[j]);
+  }
+  uint32_t w[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    w[j] = (uint32_t)f32_to_bf16(acc[2 * j]) | ((uint32_t)f32_to_bf16(acc[2 * j + 1]) << 16);
+  *reinterpret_cast<uint4*>(out + (size_t)m * H + c) = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+}  // namespace rlu
+
+extern "C" {
+
+int rlu_quant_fp8_group(const void* x, int rows, int K, int ldx, int group, void* q,
+                        float* scale, hipStream_t stream) {
+  if (rows < 0 || K <= 0 || K % 8 || ldx < K || ldx % 8) return -1;
+  if (!(group == 0 || (group == 128 && K % 128 == 0))) return -2;
+  if (group == 0 && K > rlu::QT * 8 * 64) return -3;
+  if (rows == 0) return 0;
+  hipLaunchKernelGGL(rlu::group_quant_k, dim3(rows), dim3(rlu::QT), 0, stream,
+                     (const uint16_t*)x, K, ldx, group, (uint8_t*)q, scale);
+  return (int)hipGetLastError();
+}
+
+int rlu_silu_mul_quant(const void* x, int rows, int d, int ldx, int group, void* q,
+                       float* scale, void* act, hipStream_t stream) {
+  if (rows < 0 || d <= 0 || d % 8 || ldx < 2 * d || ldx % 8) return -1;
+  if (!(group == 0 || (group == 128 && d % 128 == 0))) return -2;
+  if (group == 0 && d > rlu::QT * 8 * 4) return -3;
+  if (rows == 0) return 0;
+  hipLaunchKernelGGL(rlu::silu_mul_quant_k, dim3(rows), dim3(rlu::QT), 0, stream,
+                     (const uint16_t*)x, d, ldx, group, (uint8_t*)q, scale, (uint16_t*)act);
+  return (int)hipGetLastError();
+}
+
+int rlu_moe_sum(const void* in, int M, int top_k, int H, void* out, hipStream_t stream) {
+  if (M < 0 || top_k <= 0 || H <= 0 || H % 8) return -1;
+  if (M == 0) return 0;
+  hipLaunchKernelGGL(rlu::moe_sum_k, dim3(M, (H + rlu::QT * 8 - 1) / (rlu::QT * 8)),
+                     dim3(rlu::QT), 0, stream, (const uint16_t*)in, top_k, H, (uint16_t*)out);
+  return (int)hipGetLastError();
+}
+
+}  // extern "C"

@@ -1,0 +1,120 @@
+"""Host side of the quant, SiLU-quant, moe_sum and fp8 GEMM kernels of librlu.so.
+
+Mirrors the reference's Python entry points for these stages:
+  silu_mul_quant / supported      kernels/fused_silu_mul_quant.py:60-101
+  fp8_quant_group                 the activation quant of r4dhip.py.diff:22-34 and of
+                                  kernels/fp8_target_lmhead.py:72-73 (per token group 128)
+  moe_sum                         vLLM ops.moe_sum (r4d_mxfp4_moe.py.lru.diff:696)
+  _r4d_fp8_moe_gemm_into          the op r4d_mxfp4_moe_gemm_into (r4d_mxfp4_moe.py.lru.diff:
+                                  363-423), same argument list; ws_t = [E, N/128, K/128] fp32
+                                  block scales, x_scale = [rows, K/128]; wref unused
+  gemm_fp8_block                  kernels/fp8_target_lmhead.py:70-74
+Errors from the C-ABI raise RuntimeError; there is no fallback implementation.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from ._lib import check, lib, stream_ptr
+
+_P = ctypes.c_void_p
+FP8 = torch.float8_e4m3fn
+GROUP = 128
+MAX_ROW_PER_TOKEN = 256 * 8 * 4     # per-token SiLU-quant row limit (one workgroup)
+
+
+def _p(t: torch.Tensor | None) -> _P:
+    return _P(0 if t is None else t.data_ptr())
+
+
+def supported(x: torch.Tensor) -> bool:
+    """Whether `x` is a [rows, 2*d] gated-activation input the fused kernel handles
+    (kernels/fused_silu_mul_quant.py:60-72, with this kernel's own limits)."""
+    return (x.is_cuda and x.ndim == 2 and x.dtype == torch.bfloat16 and x.shape[1] % 16 == 0
+            and x.stride(1) == 1 and x.stride(0) % 8 == 0 and x.shape[1] // 2 <= MAX_ROW_PER_TOKEN)
+
+
+def silu_mul_quant(x: torch.Tensor, fp8_dtype: torch.dtype = FP8, write_act: bool = False,
+                   group: int = GROUP, out: tuple | None = None):
+    """silu(x[:, :d]) * x[:, d:] and its e4m3 quant in one launch -> (act|None, q, scale).
+    group=128: scale [rows, d/128]; group=0: the reference's per-token scale [rows, 1]."""
+    assert fp8_dtype == FP8, "e4m3fn only"
+    assert supported(x), "silu_mul_quant: unsupported input"
+    rows, d = x.shape[0], x.shape[1] // 2
+    if out is None:
+        q = torch.empty((rows, d), dtype=FP8, device=x.device)
+        scale = torch.empty((rows, d // group if group else 1), dtype=torch.float32,
+                            device=x.device)
+    else:
+        q, scale = out
+    act = torch.empty((rows, d), dtype=x.dtype, device=x.device) if write_act else None
+    rc = lib().rlu_silu_mul_quant(_p(x), rows, d, x.stride(0), group, _p(q), _p(scale), _p(act),
+                                  _P(stream_ptr()))
+    check(rc, "rlu_silu_mul_quant")
+    return act, q, scale
+
+
+def fp8_quant_group(x: torch.Tensor, group: int = GROUP, out: tuple | None = None):
+    """bf16 [rows, K] -> (e4m3 [rows, K], fp32 scale [rows, K/group] or [rows, 1])."""
+    assert x.dtype == torch.bfloat16 and x.ndim == 2 and x.stride(1) == 1
+    rows, K = x.shape
+    if out is None:
+        q = torch.empty((rows, K), dtype=FP8, device=x.device)
+        scale = torch.empty((rows, K // group if group else 1), dtype=torch.float32,
+                            device=x.device)
+    else:
+        q, scale = out
+    rc = lib().rlu_quant_fp8_group(_p(x), rows, K, x.stride(0), group, _p(q), _p(scale),
+                                   _P(stream_ptr()))
+    check(rc, "rlu_quant_fp8_group")
+    return q, scale
+
+
+def moe_sum(ic3: torch.Tensor, output: torch.Tensor) -> None:
+    """output[m] = sum_k ic3[m, k] for ic3 [M, top_k, H] bf16 (vLLM ops.moe_sum signature)."""
+    M, top_k, H = ic3.shape
+    assert ic3.is_contiguous() and output.is_contiguous() and output.shape == (M, H)
+    rc = lib().rlu_moe_sum(_p(ic3), M, top_k, H, _p(output), _P(stream_ptr()))
+    check(rc, "rlu_moe_sum")
+
+
+def _r4d_fp8_moe_gemm_into(y: torch.Tensor, qx: torch.Tensor, x_scale: torch.Tensor,
+                           wq: torch.Tensor, ws_t: torch.Tensor, wref: torch.Tensor | None,
+                           sorted_ids: torch.Tensor, expert_ids: torch.Tensor,
+                           num_post_pad: torch.Tensor, topk_weights: torch.Tensor | None,
+                           mtk: int, top_k: int, wv: int, sk: int, npw: int) -> None:
+    """The grouped GEMM writing into caller-owned y: only rows named in sorted_ids are
+    touched, so hot and cold subsets fill one buffer."""
+    K = qx.shape[1]
+    N = wq.shape[1]
+    assert y.shape == (mtk, N) and y.dtype == torch.bfloat16 and y.is_contiguous()
+    assert qx.dtype == FP8 and wq.dtype == FP8 and wq.shape[2] == K
+    assert x_scale.dtype == torch.float32 and ws_t.dtype == torch.float32
+    assert sorted_ids.dtype == torch.int32 and expert_ids.dtype == torch.int32
+    em = sorted_ids.numel()
+    rc = lib().r4d_gemm_moe_fp8blk_nt_b16(
+        _p(qx), _p(x_scale), _p(wq), _p(ws_t), _p(wref), _p(y), _p(sorted_ids),
+        _p(expert_ids), _p(num_post_pad), _p(topk_weights), em, mtk, top_k, K, N, wv, sk, npw,
+        _P(stream_ptr()))
+    check(rc, "r4d_gemm_moe_fp8blk_nt_b16")
+
+
+def gemm_fp8_block_q(qx: torch.Tensor, xs: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor,
+                     out: torch.Tensor | None = None, wv: int = 0, npw: int = 4) -> torch.Tensor:
+    """e4m3 [M, K] (xs [M, K/128]) x e4m3 [N, K] (ws [N/128, K/128])^T -> bf16 [M, N]."""
+    M, K = qx.shape
+    N = wq.shape[0]
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=qx.device) if out is None else out
+    rc = lib().rlu_gemm_fp8blk_m16(_p(qx), _p(xs), _p(wq), _p(ws), _p(y), M, N, K, wv, npw,
+                                   _P(stream_ptr()))
+    check(rc, "rlu_gemm_fp8blk_m16")
+    return y
+
+
+def gemm_fp8_block(x: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor) -> torch.Tensor:
+    """bf16 [M, K] @ dequant(W)^T -> bf16 [M, N]: group-128 activation quant, then the GEMM
+    (kernels/fp8_target_lmhead.py:70-74); M <= 16."""
+    qx, xs = fp8_quant_group(x.contiguous(), GROUP)
+    return gemm_fp8_block_q(qx, xs, wq, ws)

@@ -1,0 +1,389 @@
+"""GPU parity of the quant, SiLU-quant, moe_sum and fp8 GEMM kernels through the C-ABI.
+
+* quant / SiLU-quant / moe_sum: bit-exact (activations, scales, e4m3 bytes) against the oracle,
+  over the shapes and magnitude regimes of tests/k4/probe_silu_quant.py:22-53 plus the zero row;
+* grouped GEMM: within 1e-2 of max|ref| (BASELINE tolerance 2e-2) against the float64
+  dequant reference, at the MoE layer's real expert shapes (w13 [1536, 2560], w2 [2560, 768]),
+  for every tile width; the reference kernel's row contract (tests/k1/moe_ref_harness.py:282-321):
+  only live rows written (output poisoned with NaN), expert -1 skips its block, num_post_pad
+  read on the device; partition invariance (hot call + cold call == one call, bit-identical,
+  tests/lru/test_numerics_lru.py:183-198); HIP-graph replay == eager;
+* fp8 lm_head GEMM at 151936 x 2560: within tolerance and argmax equal to the fp32-dequant
+  reference's.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from conftest import gpu_case
+from oracle import fp8, gemm as ogemm
+from oracle import lru as olru
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TOL = 1e-2
+
+
+def bf16_from_np(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(torch.bfloat16).to(DEV)
+
+
+def np_from_bf16(t: torch.Tensor) -> np.ndarray:
+    return t.float().cpu().numpy()
+
+
+def u8(t: torch.Tensor) -> np.ndarray:
+    return t.view(torch.uint8).cpu().numpy()
+
+
+@pytest.fixture(scope="module")
+def ops(pkg):
+    from importlib import import_module
+    return import_module(pkg.__name__ + ".ops")
+
+
+# ---- quantizers ------------------------------------------------------------------------------
+SILU_CASES = [(r, d, s, g) for r in (1, 10, 50, 80, 2048) for d in (320, 640, 768)
+              for s in (1.0, 1e-3, 60.0) for g in (0, 128) if not (g == 128 and d % 128)]
+
+
+@pytest.mark.parametrize("rows,d,scale_in,group", SILU_CASES)
+def test_silu_mul_quant_bitexact(ops, rows, d, scale_in, group):
+    rng = np.random.default_rng(rows * 7 + d)
+    x = fp8.bf16_round(rng.standard_normal((rows, 2 * d)).astype(np.float32) * scale_in)
+    if rows >= 10:
+        x[3] = 0.0                                         # the zero row: scale floor
+    act_w, q_w, s_w = fp8.silu_mul_quant(x, group)
+    xt = bf16_from_np(x)
+    gpu_case(f"silu_mul_quant rows={rows} d={d} group={group}")
+    act, q, s = ops.silu_mul_quant(xt, write_act=True, group=group)
+    torch.cuda.synchronize()
+    assert np.array_equal(np_from_bf16(act), act_w)
+    assert np.array_equal(s.cpu().numpy(), s_w)
+    assert np.array_equal(u8(q), q_w)
+
+
+@pytest.mark.parametrize("rows", [1, 5, 20, 2048])
+@pytest.mark.parametrize("K", [128, 768, 2560])
+@pytest.mark.parametrize("group", [0, 128])
+def test_group_quant_bitexact(ops, rows, K, group):
+    rng = np.random.default_rng(rows + K)
+    x = fp8.bf16_round(rng.standard_normal((rows, K)).astype(np.float32) *
+                       rng.choice([1e-3, 1.0, 60.0]))
+    q_w, s_w = fp8.group_quant(x, group)
+    gpu_case(f"group_quant rows={rows} K={K} group={group}")
+    q, s = ops.fp8_quant_group(bf16_from_np(x), group)
+    torch.cuda.synchronize()
+    assert np.array_equal(s.cpu().numpy(), s_w)
+    assert np.array_equal(u8(q), q_w)
+
+
+@pytest.mark.parametrize("M,top_k,H", [(5, 10, 2560), (20, 10, 2560), (1, 1, 64), (3, 7, 1024)])
+def test_moe_sum_bitexact(ops, M, top_k, H):
+    rng = np.random.default_rng(M * top_k)
+    ic3 = fp8.bf16_round(rng.standard_normal((M * top_k, H)).astype(np.float32))
+    want = ogemm.moe_sum(ic3, M, top_k)
+    out = torch.empty((M, H), dtype=torch.bfloat16, device=DEV)
+    gpu_case(f"moe_sum M={M} top_k={top_k} H={H}")
+    ops.moe_sum(bf16_from_np(ic3).view(M, top_k, H), out)
+    torch.cuda.synchronize()
+    assert np.array_equal(np_from_bf16(out), want)
+
+
+# ---- grouped GEMM ----------------------------------------------------------------------------
+def make_experts(E, N, K, seed):
+    """e4m3 weights with 128x128 block scales, quantized on the GPU by the block recipe of
+    kernels/fp8_target_lmhead.py:57-64 (checked against the oracle recipe in
+    test_gpu_block_quant_matches_oracle)."""
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    w = torch.randn(E, N, K, device=DEV, generator=g) * 0.02
+    return block_quant_gpu(w)
+
+
+def block_quant_gpu(w):
+    shp = w.shape
+    N, K = shp[-2], shp[-1]
+    b = w.reshape(-1, N // 128, 128, K // 128, 128)
+    amax = b.abs().amax(dim=(2, 4)).clamp(min=1e-12)
+    ws = (amax / 448.0).float()
+    wq = (b / ws[:, :, None, :, None]).clamp(-448, 448).to(torch.float8_e4m3fn)
+    return wq.reshape(shp).contiguous(), ws.reshape(*shp[:-2], N // 128, K // 128).contiguous()
+
+
+def test_gpu_block_quant_matches_oracle():
+    """The GPU data generator follows the oracle's block recipe. torch's GPU division may differ
+    from the IEEE quotient by an ulp, so scales agree to 1 ulp and codes to one e4m3 step in a
+    few places; the recipe itself is pinned bit-exactly on the CPU (test_oracle_quant)."""
+    rng = np.random.default_rng(9)
+    w = (rng.standard_normal((256, 384)) * 0.02).astype(np.float32)
+    wq, ws = block_quant_gpu(torch.from_numpy(w).to(DEV))
+    owq, ows = fp8.block_quant_weight(w)
+    g = ws.cpu().numpy()
+    assert (np.abs(g - ows) <= np.spacing(ows)).all()
+    t = fp8.e4m3_table()
+    diff = t[u8(wq)] != t[owq]
+    assert diff.mean() < 1e-3
+    step = np.abs(t[u8(wq)][diff] - t[owq][diff]) / np.maximum(np.abs(t[owq][diff]), 2 ** -9)
+    assert (step <= 0.25).all()
+
+
+def routing(M, top_k, E, seed):
+    rng = np.random.default_rng(seed)
+    return np.stack([rng.choice(E, top_k, replace=False) for _ in range(M)]).astype(np.int32)
+
+
+def align_all(ids, E, hot=None, bs=16):
+    """moe_align over all experts (table = identity), or a hot/cold split: `hot` maps
+    expert -> slot for resident experts."""
+    mk = ids.size
+    L, NB = olru.align_sizes(mk, E, bs)
+    if hot is None:
+        table = np.arange(E, dtype=np.int32)
+        return olru.align(ids.reshape(-1), E, E, table, bs, L, NB)[:3]
+    table = np.full(E, -1, np.int32)
+    for e, s in hot.items():
+        table[e] = s
+    return olru.align(ids.reshape(-1), E, len(hot), table, bs, L, NB)
+
+
+def to_dev_i32(*arrs):
+    return [torch.from_numpy(np.ascontiguousarray(a, np.int32)).to(DEV) for a in arrs]
+
+
+@pytest.fixture(scope="module")
+def layer():
+    """One MoE layer at the real expert shapes, 40 experts."""
+    E, H, I = 40, 2560, 768
+    w13q, w13s = make_experts(E, 2 * I, H, 2)
+    w2q, w2s = make_experts(E, H, I, 3)
+    return dict(E=E, H=H, I=I, w13q=w13q, w13s=w13s, w2q=w2q, w2s=w2s)
+
+
+def ref_from(dev_wq, dev_ws, experts):
+    """numpy copies of the weights of the experts used (the oracle reads these)."""
+    wq = {e: u8(dev_wq[e]) for e in experts}
+    ws = {e: dev_ws[e].cpu().numpy() for e in experts}
+    return wq, ws
+
+
+class _Lazy:
+    def __init__(self, d):
+        self.d = d
+
+    def __getitem__(self, e):
+        return self.d[e]
+
+    @property
+    def shape(self):
+        k = next(iter(self.d))
+        return (max(self.d) + 1,) + self.d[k].shape
+
+
+def run_gemm(ops, y, qx, xs, wq, ws, align, tw, mtk, top_k, npw=4, wv=0):
+    s, e, n = align
+    ops._r4d_fp8_moe_gemm_into(y, qx, xs, wq, ws, None, s, e, n, tw, mtk, top_k, wv, 1, npw)
+
+
+@pytest.mark.parametrize("npw", [1, 2, 4, 8])
+@pytest.mark.parametrize("M", [1, 5, 20])
+def test_moe_gemm1_vs_oracle(ops, layer, npw, M):
+    E, H, I = layer["E"], layer["H"], layer["I"]
+    top_k = 10
+    ids = routing(M, top_k, E, seed=M)
+    mtk = ids.size
+    al = align_all(ids, E)
+    rng = np.random.default_rng(M + 100)
+    x = fp8.bf16_round(rng.standard_normal((M, H)).astype(np.float32))
+    qx, xs = fp8.group_quant(x, 128)
+    used = sorted(set(ids.reshape(-1).tolist()))
+    wq, ws = ref_from(layer["w13q"], layer["w13s"], used)
+    want = ogemm.moe_gemm(qx, xs, _Lazy(wq), _Lazy(ws), *al, mtk, top_k)
+    y = torch.full((mtk, 2 * I), float("nan"), dtype=torch.bfloat16, device=DEV)
+    qx_t = torch.from_numpy(qx).to(DEV).view(torch.float8_e4m3fn)
+    xs_t = torch.from_numpy(xs).to(DEV)
+    gpu_case(f"moe gemm1 M={M} npw={npw}")
+    run_gemm(ops, y, qx_t, xs_t, layer["w13q"], layer["w13s"], to_dev_i32(*al), None, mtk,
+             top_k, npw=npw)
+    torch.cuda.synchronize()
+    got = np_from_bf16(y)
+    assert not np.isnan(got).any()
+    err = ogemm.rel_err(got, want)
+    assert err <= TOL, f"rel err {err:.3e}"
+
+
+@pytest.mark.parametrize("npw", [1, 4])
+@pytest.mark.parametrize("M", [1, 5, 20])
+def test_moe_gemm2_routed_weight_vs_oracle(ops, layer, npw, M):
+    E, H, I = layer["E"], layer["H"], layer["I"]
+    top_k = 10
+    ids = routing(M, top_k, E, seed=M + 7)
+    mtk = ids.size
+    al = align_all(ids, E)
+    rng = np.random.default_rng(M + 200)
+    a = fp8.bf16_round(rng.standard_normal((mtk, I)).astype(np.float32))
+    q2, s2 = fp8.group_quant(a, 128)
+    tw = rng.random(mtk).astype(np.float32)
+    used = sorted(set(ids.reshape(-1).tolist()))
+    wq, ws = ref_from(layer["w2q"], layer["w2s"], used)
+    want = ogemm.moe_gemm(q2, s2, _Lazy(wq), _Lazy(ws), *al, mtk, 1, tw=tw)
+    y = torch.full((mtk, H), float("nan"), dtype=torch.bfloat16, device=DEV)
+    gpu_case(f"moe gemm2 M={M} npw={npw}")
+    run_gemm(ops, y, torch.from_numpy(q2).to(DEV).view(torch.float8_e4m3fn),
+             torch.from_numpy(s2).to(DEV), layer["w2q"], layer["w2s"], to_dev_i32(*al),
+             torch.from_numpy(tw).to(DEV), mtk, 1, npw=npw)
+    torch.cuda.synchronize()
+    err = ogemm.rel_err(np_from_bf16(y), want)
+    assert err <= TOL, f"rel err {err:.3e}"
+
+
+def test_moe_gemm_row_contract(ops, layer):
+    """tests/k1/moe_ref_harness.py:282-321: only live rows written; expert -1 skips its block;
+    num_post_pad is honoured on the device."""
+    E, H, I = layer["E"], layer["H"], layer["I"]
+    M, top_k = 8, 10
+    ids = routing(M, top_k, E, seed=11)
+    mtk = ids.size
+    s, e, n = align_all(ids, E)
+    x = fp8.bf16_round(np.random.default_rng(1).standard_normal((M, H)).astype(np.float32))
+    qx, xs = fp8.group_quant(x, 128)
+    qx_t = torch.from_numpy(qx).to(DEV).view(torch.float8_e4m3fn)
+    xs_t = torch.from_numpy(xs).to(DEV)
+
+    def written(s_, e_, n_):
+        y = torch.full((mtk, 2 * I), float("nan"), dtype=torch.bfloat16, device=DEV)
+        run_gemm(ops, y, qx_t, xs_t, layer["w13q"], layer["w13s"], to_dev_i32(s_, e_, n_), None,
+                 mtk, top_k)
+        torch.cuda.synchronize()
+        return ~torch.isnan(y).any(dim=1).cpu().numpy(), y
+
+    gpu_case("moe gemm row contract")
+    w0, y0 = written(s, e, n)
+    live = np.zeros(mtk, bool)
+    live[s[:n[0]][s[:n[0]] < mtk]] = True
+    assert np.array_equal(w0, live)
+    e2 = e.copy()
+    e2[0] = -1
+    w2, y2 = written(s, e2, n)
+    b0 = s[:16][s[:16] < mtk]
+    assert not w2[b0].any()
+    others = live.copy()
+    others[b0] = False
+    assert torch.equal(y2[torch.from_numpy(others).to(DEV)], y0[torch.from_numpy(others).to(DEV)])
+    w3, _ = written(s, e, np.array([16], np.int32))
+    assert np.array_equal(np.nonzero(w3)[0], np.sort(b0))
+
+
+def test_moe_gemm_partition_invariance(ops, layer):
+    """hot call (slot buffers) + cold call (full tensor) into one y == one all-cold call,
+    bit for bit (tests/lru/test_numerics_lru.py:183-198), output poisoned with NaN first."""
+    E, H, I = layer["E"], layer["H"], layer["I"]
+    M, top_k = 5, 10
+    ids = routing(M, top_k, E, seed=21)
+    mtk = ids.size
+    hot_experts = sorted(set(ids.reshape(-1).tolist()))[::2]
+    hot = {ex: i for i, ex in enumerate(hot_experts)}
+    sh, eh, nh, sc, ec, nc = align_all(ids, E, hot)
+    slots_q = layer["w13q"][torch.tensor(hot_experts, device=DEV)].contiguous()
+    slots_s = layer["w13s"][torch.tensor(hot_experts, device=DEV)].contiguous()
+    x = fp8.bf16_round(np.random.default_rng(2).standard_normal((M, H)).astype(np.float32))
+    qx, xs = fp8.group_quant(x, 128)
+    qx_t = torch.from_numpy(qx).to(DEV).view(torch.float8_e4m3fn)
+    xs_t = torch.from_numpy(xs).to(DEV)
+    y = torch.full((mtk, 2 * I), float("nan"), dtype=torch.bfloat16, device=DEV)
+    gpu_case("moe gemm partition invariance")
+    run_gemm(ops, y, qx_t, xs_t, slots_q, slots_s, to_dev_i32(sh, eh, nh), None, mtk, top_k)
+    run_gemm(ops, y, qx_t, xs_t, layer["w13q"], layer["w13s"], to_dev_i32(sc, ec, nc), None,
+             mtk, top_k)
+    y1 = torch.full_like(y, float("nan"))
+    run_gemm(ops, y1, qx_t, xs_t, layer["w13q"], layer["w13s"], to_dev_i32(*align_all(ids, E)),
+             None, mtk, top_k)
+    torch.cuda.synchronize()
+    assert not torch.isnan(y).any()
+    assert torch.equal(y.view(torch.int16), y1.view(torch.int16))
+
+
+def test_moe_gemm_graph_replay(ops, layer):
+    E, H, I = layer["E"], layer["H"], layer["I"]
+    M, top_k = 5, 10
+    ids = routing(M, top_k, E, seed=31)
+    mtk = ids.size
+    al = to_dev_i32(*align_all(ids, E))
+    qx_t = torch.zeros((M, H), dtype=torch.float8_e4m3fn, device=DEV)
+    xs_t = torch.ones((M, H // 128), dtype=torch.float32, device=DEV)
+    y = torch.empty((mtk, 2 * I), dtype=torch.bfloat16, device=DEV)
+    rng = np.random.default_rng(3)
+    inputs = []
+    for _ in range(3):
+        x = fp8.bf16_round(rng.standard_normal((M, H)).astype(np.float32))
+        q, s_ = fp8.group_quant(x, 128)
+        inputs.append((torch.from_numpy(q).to(DEV).view(torch.float8_e4m3fn),
+                       torch.from_numpy(s_).to(DEV)))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run_gemm(ops, y, qx_t, xs_t, layer["w13q"], layer["w13s"], al, None, mtk, top_k)
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    gpu_case("moe gemm graph capture")
+    with torch.cuda.graph(g):
+        run_gemm(ops, y, qx_t, xs_t, layer["w13q"], layer["w13s"], al, None, mtk, top_k)
+    for q, s_ in inputs:
+        qx_t.copy_(q)
+        xs_t.copy_(s_)
+        g.replay()
+        torch.cuda.synchronize()
+        ye = torch.empty_like(y)
+        run_gemm(ops, ye, q, s_, layer["w13q"], layer["w13s"], al, None, mtk, top_k)
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), ye.view(torch.int16))
+
+
+def test_moe_gemm_return_codes(ops, layer):
+    y = torch.empty((10, 1536), dtype=torch.bfloat16, device=DEV)
+    q = torch.zeros((1, 2560), dtype=torch.float8_e4m3fn, device=DEV)
+    s = torch.zeros((1, 20), dtype=torch.float32, device=DEV)
+    al = to_dev_i32(np.zeros(16), np.zeros(1), np.zeros(1))
+    for wv, sk, npw, want in ((0, 2, 4, -4), (0, 1, 3, -6), (17, 1, 4, -5)):
+        with pytest.raises(RuntimeError, match=f"rc={want}"):
+            ops._r4d_fp8_moe_gemm_into(y, q, s, layer["w13q"], layer["w13s"], None, *al, None,
+                                       10, 10, wv, sk, npw)
+
+
+# ---- fp8 lm_head -----------------------------------------------------------------------------
+@pytest.fixture(scope="module")
+def lm_head():
+    N, K = 151936, 2560
+    g = torch.Generator(device=DEV).manual_seed(5)
+    w = torch.randn(N, K, device=DEV, generator=g) * 0.02
+    wq, ws = block_quant_gpu(w)
+    del w
+    return wq, ws
+
+
+@pytest.mark.parametrize("M", [1, 5, 8, 16])
+def test_fp8_lmhead_vs_dequant_reference(ops, lm_head, M):
+    wq, ws = lm_head
+    N, K = wq.shape
+    rng = np.random.default_rng(M + 4)
+    x = fp8.bf16_round(rng.standard_normal((M, K)).astype(np.float32))
+    xt = bf16_from_np(x)
+    gpu_case(f"fp8 lm_head M={M}")
+    y = ops.gemm_fp8_block(xt, wq, ws)
+    torch.cuda.synchronize()
+    qx, xs = fp8.group_quant(x, 128)
+    a = torch.from_numpy(fp8.dequant_act(qx, xs)).to(DEV).double()
+    wd = (wq.float() * ws.repeat_interleave(128, 0).repeat_interleave(128, 1)).double()
+    ref = a @ wd.T
+    del wd
+    err = ((y.double() - ref).abs().max() / ref.abs().max()).item()
+    assert err <= TOL, f"rel err {err:.3e}"
+    am, ar = y.float().argmax(1), ref.argmax(1)
+    # argmax must match, unless the reference's top two are closer than one bf16 step
+    for r in range(M):
+        if am[r] != ar[r]:
+            gap = (ref[r, ar[r]] - ref[r, am[r]]).abs().item()
+            assert gap <= 2 ** -7 * ref[r, ar[r]].abs().item(), (r, gap)
