@@ -1,0 +1,387 @@
+#!/usr/bin/env python3
+"""MoE decode step on one MI355X: device LRU cache + align + fp8 grouped expert GEMMs.
+
+Workload (the 52-layer decode step): 52 MoE layers, E=512 experts of hidden 2560 /
+intermediate 768 (w13 [1536, 2560], w2 [2560, 768], fp8 e4m3 with 128x128 float32 block scales,
+weights ~N(0, 0.02) before quantization), S=257 HBM slots per layer warm-started from the
+hottest experts of each layer's routing, top-10 routing of B=4 streams x 5 rows (MTP-4) = 20
+tokens per step from a seeded Zipf(1.1) trace per layer (seed 1000 + layer, rows correlated so a
+layer sees 5-13 misses per step). Per layer and step: r4d_lru_fused (manager + both aligns),
+group-128 activation quant, gate_up GEMM (hot slots + cold tensor), SiLU-mul-quant, down GEMM
+with routed weights, moe_sum -- captured once as a HIP graph and replayed with new routing.
+
+`value` is ms per 52-layer step with every input resident in HBM: the miss gather, which reads
+pinned host memory over PCIe, is timed in a second graph and reported as
+`e2e_with_gather_ms_per_step`; the same step at B=1 (5 tokens) is `b1_ms_per_step`.
+
+    python bench.py [--steps K] [--warmup W] [--only-b4]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import pathlib
+import platform
+import sys
+import time
+
+import numpy as np
+
+ROOT = pathlib.Path(__file__).resolve().parent
+PKG_NAME = "r9700_lru_expert_cache_amd"
+
+METRIC = "MoE decode ms/step (LRU+align+grouped GEMM) B=1/4; % HBM roofline"
+E, S, H, I, TOPK, LAYERS = 512, 257, 2560, 768, 10, 52
+EXPERT_BYTES = 2 * I * H + H * I + (2 * I // 128) * (H // 128) * 4 + (H // 128) * (I // 128) * 4
+HBM_PEAK_GBS = 8000.0
+
+
+def load_pkg():
+    import importlib.util
+    if PKG_NAME in sys.modules:
+        return sys.modules[PKG_NAME]
+    d = ROOT / "r9700-lru-expert-cache_amd"
+    spec = importlib.util.spec_from_file_location(PKG_NAME, d / "__init__.py",
+                                                  submodule_search_locations=[str(d)])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules[PKG_NAME] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# ---- workload ---------------------------------------------------------------------------------
+def make_pool(torch, dev):
+    """512 experts, fp8 + block scales, quantized on the GPU (chunks of 32 experts)."""
+    def quant(w):
+        n, k = w.shape[-2], w.shape[-1]
+        b = w.reshape(w.shape[0], n // 128, 128, k // 128, 128)
+        ws = (b.abs().amax(dim=(2, 4)).clamp(min=1e-12) / 448.0).float()
+        wq = (b / ws[:, :, None, :, None]).clamp(-448, 448).to(torch.float8_e4m3fn)
+        return wq.reshape(w.shape), ws
+    g = torch.Generator(device=dev).manual_seed(2)
+    out = {}
+    for name, (n, k) in (("w13", (2 * I, H)), ("w2", (H, I))):
+        wq = torch.empty((E, n, k), dtype=torch.float8_e4m3fn, device=dev)
+        ws = torch.empty((E, n // 128, k // 128), dtype=torch.float32, device=dev)
+        for e0 in range(0, E, 32):
+            q, s = quant(torch.randn(32, n, k, device=dev, generator=g) * 0.02)
+            wq[e0:e0 + 32] = q
+            ws[e0:e0 + 32] = s
+        out[name], out[name + "s"] = wq, ws
+    return out
+
+
+def layer_trace(layer, rows, steps):
+    from oracle import trace
+    corr = 0.7 if rows >= 20 else 0.0
+    return trace.zipf_trace(seed=1000 + layer, E=E, rows=rows, k=TOPK, steps=steps, s=1.1,
+                            corr=corr)
+
+
+def build(torch, pkg, rows, steps, dev, pool_dev, host_full, layers_cache=None):
+    """Layers (slots shared between batch sizes: the hot set depends only on the layer seed)."""
+    from oracle import trace
+    ids = np.empty((steps, LAYERS, rows, TOPK), np.int32)
+    layers = []
+    for l in range(LAYERS):
+        tr, perm0 = layer_trace(l, rows, steps)
+        ids[:, l] = tr.reshape(steps, rows, TOPK)
+        hot, rank = trace.warm_hot(perm0, S)
+        if layers_cache is not None and l < len(layers_cache):
+            slots = layers_cache[l].slots
+        else:
+            idx = torch.tensor(sorted(hot.tolist()), dtype=torch.int64, device=dev)
+            slots = pkg.ExpertWeights(*[pool_dev[n].index_select(0, idx).contiguous()
+                                        for n in ("w13", "w13s", "w2", "w2s")])
+        layers.append(pkg.LruMoELayer(host_full, hot, rank, rows, TOPK, dev, slots=slots))
+    return layers, ids
+
+
+def capture(torch, layers, ids_static, tw, hbuf, gather, side):
+    def step():
+        for l, layer in enumerate(layers):
+            layer.apply(hbuf[l + 1], hbuf[l], tw, ids_static[l], gather=gather, side=side)
+    # one eager step first (loads every kernel), then the cache state is put back
+    snap = snapshot(torch, layers)
+    step()
+    torch.cuda.synchronize()
+    restore(layers, snap)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    torch.cuda.synchronize()
+    return g
+
+
+def snapshot(torch, layers):
+    return [[t.clone() for t in L.cache.state()] for L in layers]
+
+
+def restore(layers, snap):
+    for L, s in zip(layers, snap):
+        for t, v in zip(L.cache.state(), s):
+            t.copy_(v)
+
+
+def run_steps(torch, g, ids_dev, ids_static, t0, k):
+    for t in range(t0, t0 + k):
+        ids_static.copy_(ids_dev[t])
+        g.replay()
+
+
+def time_steps(torch, g, ids_dev, ids_static, t0, k):
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    w0 = time.perf_counter()
+    a.record()
+    run_steps(torch, g, ids_dev, ids_static, t0, k)
+    b.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - w0
+    return a.elapsed_time(b) / k, wall
+
+
+def distinct_per_layer(ids_step):
+    """distinct experts routed per layer for one step [LAYERS, rows, TOPK]."""
+    return np.array([len(np.unique(ids_step[l])) for l in range(ids_step.shape[0])])
+
+
+def gemm_roofline(torch, pkg, layers, ids_last, rows, reps=3):
+    """Average duration of the grouped GEMM launches of one step (both GEMMs of all 52 layers,
+    eager, back to back on the current stream, HIP events around them) and the algorithmic
+    bytes each launch moves: every distinct expert's weights and scales once, the activations
+    and scales once, the output rows once."""
+    mtk = rows * TOPK
+    n = 0
+    bytes_total = 0.0
+    d = distinct_per_layer(ids_last)
+    for l, L in enumerate(layers):
+        e = int(d[l])
+        bytes_total += (e * (2 * I * H + (2 * I // 128) * (H // 128) * 4)
+                        + rows * H + rows * (H // 128) * 4 + mtk * 2 * I * 2)        # GEMM1
+        bytes_total += (e * (H * I + (H // 128) * (I // 128) * 4)
+                        + mtk * I + mtk * (I // 128) * 4 + mtk * H * 2 + mtk * 4)     # GEMM2
+        n += 2
+    per_launch_bytes = bytes_total / n
+
+    def launches():
+        for L in layers:
+            L._gemm_split(L.ic1, L.qx, L.xs, L.slots.w13, L.slots.s13, L.full_ptrs[0],
+                          L.full_ptrs[1], None, L.top_k, L.npw1)
+            L._gemm_split(L.ic3, L.q2, L.s2, L.slots.w2, L.slots.s2, L.full_ptrs[2],
+                          L.full_ptrs[3], L.tw, 1, L.npw2)
+    launches()
+    torch.cuda.synchronize()
+    best = 1e30
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        launches()
+        b.record()
+        torch.cuda.synchronize()
+        best = min(best, a.elapsed_time(b) * 1e3 / n)
+    gbs = per_launch_bytes / (best * 1e-6) / 1e9
+    return dict(bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                frac=round(gbs / HBM_PEAK_GBS, 4), traffic=None,
+                kernel="rlu::moe_gemm_k<4, false> (gate_up and down, hot+cold in one launch)",
+                avg_launch_us=round(best, 2), algorithmic_bytes_per_launch=int(per_launch_bytes),
+                distinct_experts_per_layer=round(float(d.mean()), 1))
+
+
+def lru_us_per_layer(torch, layers, ids_dev, ids_static, t, reps=5):
+    """The fused LRU kernel alone for all 52 layers (state restored afterwards)."""
+    snap = snapshot(torch, layers)
+    ids_static.copy_(ids_dev[t])
+    def go():
+        for l, L in enumerate(layers):
+            L.cache.fused(ids_static[l], out=L.align)
+    go()
+    torch.cuda.synchronize()
+    best = 1e30
+    for _ in range(reps):
+        restore(layers, snap)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        go()
+        b.record()
+        torch.cuda.synchronize()
+        best = min(best, a.elapsed_time(b) * 1e3 / len(layers))
+    restore(layers, snap)
+    return best
+
+
+# ---- CPU baseline: the oracle restatement of one layer step, timed on the host ------------------
+def cpu_baseline(pool_cpu_w13, pool_cpu_w2, ids, budget_s=10.0):
+    from oracle import fp8, lru as olru, gemm as ogemm
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
+    except Exception:  # noqa: BLE001
+        threads = 1
+    rows = ids.shape[2]
+    mtk = rows * TOPK
+    rng = np.random.default_rng(1)
+    x = fp8.bf16_round(rng.standard_normal((rows, H)).astype(np.float32))
+    tw = rng.random(mtk).astype(np.float32)
+    from oracle import trace
+    done = 0
+    t0 = time.perf_counter()
+    per = []
+    while time.perf_counter() - t0 < budget_s and done < LAYERS:
+        l = done
+        _, perm0 = layer_trace(l, rows, 1)
+        hot, rank = trace.warm_hot(perm0, S)
+        st = olru.warm_start(E, S, hot, rank)
+        tl = time.perf_counter()
+        al = olru.fused(st, ids[0, l].reshape(-1), 16)
+        qx, xs = fp8.group_quant(x, 128)
+        used = np.unique(ids[0, l])
+        W13 = {int(e): pool_cpu_w13[int(e)] for e in used}
+        W2 = {int(e): pool_cpu_w2[int(e)] for e in used}
+        table = np.arange(E, dtype=np.int32)
+        a_all = olru.align(ids[0, l].reshape(-1), E, E, table, 16, *olru.align_sizes(mtk, E, 16))
+        y1 = ogemm.moe_gemm(qx, xs, _Dict(W13, 0), _Dict(W13, 1), *a_all[:3], mtk, TOPK)
+        _, q2, s2 = fp8.silu_mul_quant(fp8.bf16_round(y1.astype(np.float32)), 128)
+        y2 = ogemm.moe_gemm(q2, s2, _Dict(W2, 0), _Dict(W2, 1), *a_all[:3], mtk, 1, tw=tw)
+        ogemm.moe_sum(fp8.bf16_round(y2.astype(np.float32)), rows, TOPK)
+        per.append(time.perf_counter() - tl)
+        done += 1
+    ms_layer = 1e3 * float(np.median(per))
+    return dict(value=round(ms_layer * LAYERS, 1), unit="ms/step", cores=int(threads),
+                kind="port",
+                sample=f"{done} of the 52 layers of one B={rows // 5} step through the numpy "
+                       f"oracle (fused LRU + align, group quant, fp32-dequant GEMMs in float64, "
+                       f"SiLU-quant, moe_sum); median layer time x 52",
+                cpu=platform.processor() or platform.machine(), os_cpu_count=os.cpu_count())
+
+
+class _Dict:
+    """expert -> (wq, ws) numpy pair, indexed like the [E, ...] arrays the oracle expects."""
+    def __init__(self, d, which):
+        self.d, self.w = d, which
+
+    def __getitem__(self, e):
+        return self.d[int(e)][self.w]
+
+    @property
+    def shape(self):
+        k = next(iter(self.d))
+        return (E,) + self.d[k][self.w].shape
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--only-b4", action="store_true",
+                    help="only the B=4 HBM-resident step (the profiled command)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this path runs on one GPU; --gpus must be 1 (multi-GPU "
+                                   "sharding is described in DESIGN.md, not launched)"}))
+        sys.exit(2)
+    if int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py runs on one GPU only", file=sys.stderr)
+        sys.exit(2)
+    sys.path.insert(0, str(ROOT))
+    import torch
+    pkg = load_pkg()
+    pkg.lib()                                   # fail loudly without the HIP library
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    t_setup = time.perf_counter()
+    log("generating 512 fp8 experts")
+    pool = make_pool(torch, dev)
+    host = {n: torch.empty(t.shape, dtype=t.dtype, pin_memory=True) for n, t in pool.items()}
+    for n in pool:
+        host[n].copy_(pool[n])
+    host_full = pkg.ExpertWeights(host["w13"], host["w13s"], host["w2"], host["w2s"])
+    T = args.warmup + 3 * args.steps + 2
+    rows4 = 20
+    log(f"building {LAYERS} layers (B=4, {rows4} tokens)")
+    layers4, ids4 = build(torch, pkg, rows4, T, dev, pool, host_full)
+    # numpy views of the pinned pool (no copies) for the CPU baseline
+    cpu_w13 = _Pair(host["w13"].view(torch.uint8).numpy(), host["w13s"].numpy())
+    cpu_w2 = _Pair(host["w2"].view(torch.uint8).numpy(), host["w2s"].numpy())
+    del pool
+    torch.cuda.empty_cache()
+    g = torch.Generator().manual_seed(3)
+    tw4 = torch.softmax(torch.randn(rows4, TOPK, generator=g), -1).to(dev)
+    hb4 = torch.empty((LAYERS + 1, rows4, H), dtype=torch.bfloat16, device=dev)
+    hb4[0] = torch.randn(rows4, H, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
+    ids4_dev = torch.from_numpy(ids4).to(dev)
+    ids4_static = torch.empty_like(ids4_dev[0])
+    side = torch.cuda.Stream()
+    ids4_static.copy_(ids4_dev[0])
+    gB = capture(torch, layers4, ids4_static, tw4, hb4, gather=False, side=side)
+    log(f"setup {time.perf_counter() - t_setup:.1f}s; warmup {args.warmup} steps")
+    run_steps(torch, gB, ids4_dev, ids4_static, 0, args.warmup)
+    t = args.warmup
+    ms4, wall4 = time_steps(torch, gB, ids4_dev, ids4_static, t, args.steps)
+    t += args.steps
+    log(f"B=4 HBM-resident step: {ms4:.3f} ms")
+    roof = gemm_roofline(torch, pkg, layers4, ids4[t - 1], rows4)
+    lru_us = lru_us_per_layer(torch, layers4, ids4_dev, ids4_static, t)
+    out = {"metric": METRIC, "value": round(ms4, 4), "unit": "ms/step", "n_gpus": 1,
+           "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms4, 4),
+           "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+           "dtype": "fp8e4m3", "data": "synthetic",
+           "config": {"workload": f"{LAYERS}-layer MoE decode step, B=4 (20 tokens), top-10 of "
+                                  f"E=512, S=257 HBM slots/layer, w13 [1536,2560] + w2 "
+                                  f"[2560,768] fp8 e4m3 128x128-block-scaled, Zipf(1.1) routing "
+                                  f"with 5-13 misses/layer/step",
+                      "layers": LAYERS, "tokens": rows4, "top_k": TOPK, "experts": E,
+                      "slots": S, "hidden": H, "moe_intermediate": I},
+           "roofline": roof, "lru_fused_us_per_layer": round(lru_us, 2),
+           "wall_s_timed": round(wall4, 3)}
+    if not args.only_b4:
+        gA = capture(torch, layers4, ids4_static, tw4, hb4, gather=True, side=side)
+        run_steps(torch, gA, ids4_dev, ids4_static, t, 1)
+        t += 1
+        mse, _ = time_steps(torch, gA, ids4_dev, ids4_static, t, args.steps)
+        t += args.steps
+        out["e2e_with_gather_ms_per_step"] = round(mse, 3)
+        # misses per layer in the last step, from the device state
+        nm = [int(L.cache.n_miss.item()) for L in layers4]
+        out["misses_per_layer_last_step"] = round(float(np.mean(nm)), 2)
+        log(f"B=4 with PCIe miss gather: {mse:.3f} ms")
+        del gA, gB
+        torch.cuda.synchronize()
+        # B=1: same layers' slots, fresh caches, 5 tokens
+        rows1 = 5
+        layers1, ids1 = build(torch, pkg, rows1, args.warmup + args.steps + 1, dev, None,
+                              host_full, layers_cache=layers4)
+        tw1 = torch.softmax(torch.randn(rows1, TOPK, generator=g), -1).to(dev)
+        hb1 = torch.empty((LAYERS + 1, rows1, H), dtype=torch.bfloat16, device=dev)
+        hb1[0] = hb4[0, :rows1]
+        ids1_dev = torch.from_numpy(ids1).to(dev)
+        ids1_static = torch.empty_like(ids1_dev[0])
+        ids1_static.copy_(ids1_dev[0])
+        g1 = capture(torch, layers1, ids1_static, tw1, hb1, gather=False, side=side)
+        run_steps(torch, g1, ids1_dev, ids1_static, 0, args.warmup)
+        ms1, _ = time_steps(torch, g1, ids1_dev, ids1_static, args.warmup, args.steps)
+        out["b1_ms_per_step"] = round(ms1, 4)
+        log(f"B=1 HBM-resident step: {ms1:.3f} ms")
+        out["cpu_baseline"] = cpu_baseline(cpu_w13, cpu_w2, ids4, args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+class _Pair:
+    """expert -> (e4m3 bytes, block scales) from the [E, ...] pool arrays."""
+    def __init__(self, wq, ws):
+        self.wq, self.ws = wq, ws
+
+    def __getitem__(self, e):
+        return self.wq[int(e)], self.ws[int(e)]
+
+
+if __name__ == "__main__":
+    main()

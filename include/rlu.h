@@ -93,15 +93,30 @@ int rlu_moe_sum(const void* in, int M, int top_k, int H, void* out, hipStream_t 
  *   expert_ids [em/16], num_post_pad [1] (read on the device), topk_weights [mtk] f32 or null.
  * Row contract of the reference kernel: sorted ids >= mtk are padding, expert id -1 skips the
  * block, only named rows are written, y[row] *= topk_weights[row] when given.
- * wv = workgroups per CU of the persistent grid (0: 4), sk = split-K (must be 1), npw =
- * 16-column tiles per wave (1, 2, 4, 8). Returns -1 bad sizes, -2 K or N not a multiple of
- * 128, -4 sk != 1, -5 bad wv, -6 bad npw; the closed launcher aborted instead. */
+ * wv = workgroups per CU of the persistent grid (0: 3), sk = waves of a workgroup that split
+ * one tile's K range (1, 2, 4; 0: the largest that divides K/128), npw = 16-column tiles per
+ * item (1, 2, 4, 8). Partial sums are added in a fixed order, so a given sk is deterministic.
+ * Returns -1 bad sizes, -2 K or N not a multiple of 128, -4 sk unsupported or not dividing
+ * K/128, -5 bad wv, -6 bad npw; the closed launcher aborted instead. */
 int r4d_gemm_moe_fp8blk_nt_b16(const void* qx, const float* xs, const void* wq,
                                const float* ws, const void* wref, void* y,
                                const int* sorted_ids, const int* expert_ids,
                                const int* num_post_pad, const float* topk_weights, int em,
                                int mtk, int top_k, int K, int N, int wv, int sk, int npw,
                                hipStream_t stream);
+
+/* No counterpart in the reference as one call: the two r4d_mxfp4_moe_gemm_into calls of
+ * _gemm_split (patches/.../r4d_mxfp4_moe.py.lru.diff:584-592) -- resident slots, then the full
+ * expert tensor -- in one launch. Block list 1 (sorted_hot, eids_hot, npad_hot, em entries)
+ * runs against wq_hot / ws_hot, block list 2 against wq / ws (device or pinned host memory).
+ * Same row contract, checks and codes as r4d_gemm_moe_fp8blk_nt_b16 with sk = 0, so its output
+ * equals the two sk = 0 calls bit for bit. */
+int rlu_moe_gemm_split(const void* qx, const float* xs, const void* wq_hot, const float* ws_hot,
+                       const int* sorted_hot, const int* eids_hot, const int* npad_hot,
+                       const void* wq, const float* ws, const int* sorted_cold,
+                       const int* eids_cold, const int* npad_cold, const float* topk_weights,
+                       void* y, int em, int mtk, int top_k, int K, int N, int wv, int npw,
+                       hipStream_t stream);
 
 /* Replaces fp8hip_gemm_w8a8_launch behind gemm_fp8_block (kernels/fp8_target_lmhead.py:70-74):
  * y [M, N] bf16 = qx [M, K] (xs [M, K/128]) x w [N, K] (ws [N/128, K/128])^T, 1 <= M <= 16. */

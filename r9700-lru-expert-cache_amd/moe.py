@@ -1,0 +1,149 @@
+"""One MoE layer of the decode hot path: device LRU cache, align, miss gather and the fp8 expert
+GEMMs, all on librlu.so.
+
+Mirrors R4dMxfp4MoEExperts' split path (patches/model_executor/layers/fused_moe/experts/
+r4d_mxfp4_moe.py.lru.diff): _build_hot / _build_lru (:453-541) -> LruMoELayer.__init__,
+_lru_step_fused (:557-579) -> _lru_step_fused, _gemm_split (:584-607) -> _gemm_split,
+_act_quant (:640-657) -> _act_quant, _apply_split (:659-696) -> apply. The experts are fp8 e4m3
+with 128x128 float32 block scales (w13 [E, 2I, H], w2 [E, H, I]); the activation quant is
+per-token-group-128. The miss gather runs on a side stream and the GEMMs wait for it.
+
+Every buffer a step touches is allocated here, once, for a fixed token count, so a step can be
+captured into a HIP graph and replayed with new routing (only contents change).
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import ops
+from ._lib import check, lib, stream_ptr
+from .lru import LRU_CHUNKS, LRU_LANES, LruCache, _r4d_lru_gather
+
+_P = ctypes.c_void_p
+BLOCK = 16
+
+
+def device_ptr_of_pinned(t: torch.Tensor) -> int:
+    """Device-visible address of a pinned host tensor (UVA)."""
+    hip = ctypes.CDLL("libamdhip64.so")
+    dp = ctypes.c_void_p()
+    rc = hip.hipHostGetDevicePointer(ctypes.byref(dp), ctypes.c_void_p(t.data_ptr()),
+                                     ctypes.c_uint(0))
+    if rc != 0:
+        raise RuntimeError(f"hipHostGetDevicePointer rc={rc}")
+    return dp.value
+
+
+@dataclass
+class ExpertWeights:
+    """fp8 experts with block scales; the four per-expert buffers of the fp8 format."""
+    w13: torch.Tensor     # e4m3 [E, 2I, H]
+    s13: torch.Tensor     # f32  [E, 2I/128, H/128]
+    w2: torch.Tensor      # e4m3 [E, H, I]
+    s2: torch.Tensor      # f32  [E, H/128, I/128]
+
+    def tensors(self):
+        return [self.w13, self.s13, self.w2, self.s2]
+
+    def ptrs(self) -> list[int]:
+        """Device-visible addresses (pinned host tensors are translated)."""
+        return [device_ptr_of_pinned(t) if t.is_pinned() else t.data_ptr()
+                for t in self.tensors()]
+
+
+class LruMoELayer:
+    def __init__(self, full: ExpertWeights, hot_ids, rank: dict | None, max_tokens: int,
+                 top_k: int, device="cuda", slots: ExpertWeights | None = None,
+                 npw1: int = 4, npw2: int = 4, wv: int = 0):
+        dev = torch.device(device)
+        self.full = full
+        self.full_ptrs = full.ptrs()
+        self.E = full.w13.shape[0]
+        self.N1, self.H = full.w13.shape[1], full.w13.shape[2]
+        self.I = self.N1 // 2
+        self.top_k = top_k
+        self.M = max_tokens
+        self.mtk = max_tokens * top_k
+        self.npw1, self.npw2, self.wv = npw1, npw2, wv
+        hot = sorted(int(e) for e in hot_ids)
+        if slots is None:
+            idx = torch.tensor(hot, dtype=torch.int64)
+            slots = ExpertWeights(*[t.index_select(0, idx.to(t.device)).to(dev).contiguous()
+                                    for t in full.tensors()])
+        self.slots = slots
+        self.cache = LruCache.build(self.E, hot, rank, dev)
+        # align outputs and intermediates for exactly max_tokens rows
+        self.align = self.cache.alloc_align(self.mtk, BLOCK)
+        self.qx = torch.empty((self.M, self.H), dtype=ops.FP8, device=dev)
+        self.xs = torch.empty((self.M, self.H // 128), dtype=torch.float32, device=dev)
+        self.ic1 = torch.empty((self.mtk, self.N1), dtype=torch.bfloat16, device=dev)
+        self.q2 = torch.empty((self.mtk, self.I), dtype=ops.FP8, device=dev)
+        self.s2 = torch.empty((self.mtk, self.I // 128), dtype=torch.float32, device=dev)
+        self.ic3 = torch.empty((self.mtk, self.H), dtype=torch.bfloat16, device=dev)
+        self.tw = torch.empty((self.mtk,), dtype=torch.float32, device=dev)
+
+    # -- _lru_step_fused: manager + both aligns in one launch, then the miss gather -----------
+    def _lru_step_fused(self, topk_ids: torch.Tensor, gather: bool, side: torch.cuda.Stream | None):
+        self.cache.fused(topk_ids, out=self.align, block_size=BLOCK)
+        if not gather:
+            return None
+        # six-buffer ABI of the reference gather: the fp8 format has four per-expert buffers,
+        # the two spare pairs repeat the (small) scale buffers
+        dsts = [self.slots.w13, self.slots.w2, self.slots.s13, self.slots.s2,
+                self.slots.s13, self.slots.s2]
+        srcs = [self.full.w13, self.full.w2, self.full.s13, self.full.s2,
+                self.full.s13, self.full.s2]
+        sp = [self.full_ptrs[0], self.full_ptrs[2], self.full_ptrs[1], self.full_ptrs[3],
+              self.full_ptrs[1], self.full_ptrs[3]]
+        cur = torch.cuda.current_stream()
+        if side is None:
+            _r4d_lru_gather(dsts, srcs, self.cache.miss, self.cache.n_miss, LRU_CHUNKS,
+                            LRU_LANES, src_ptrs=sp)
+            return None
+        side.wait_stream(cur)
+        with torch.cuda.stream(side):
+            _r4d_lru_gather(dsts, srcs, self.cache.miss, self.cache.n_miss, LRU_CHUNKS,
+                            LRU_LANES, src_ptrs=sp)
+        return side
+
+    # -- _gemm_split: resident slots + the full tensor, one launch ----------------------------
+    def _gemm_split(self, y, qx, xs, slot_w, slot_s, full_w_ptr, full_s_ptr, tw, top_k, npw):
+        sh, eh, nh, sc, ec, nc = self.align
+        K = qx.shape[1]
+        N = slot_w.shape[1]
+        rc = lib().rlu_moe_gemm_split(
+            _P(qx.data_ptr()), _P(xs.data_ptr()), _P(slot_w.data_ptr()), _P(slot_s.data_ptr()),
+            _P(sh.data_ptr()), _P(eh.data_ptr()), _P(nh.data_ptr()), _P(full_w_ptr),
+            _P(full_s_ptr), _P(sc.data_ptr()), _P(ec.data_ptr()), _P(nc.data_ptr()),
+            _P(0 if tw is None else tw.data_ptr()), _P(y.data_ptr()), sh.numel(),
+            y.shape[0], top_k, K, N, self.wv, npw, _P(stream_ptr()))
+        check(rc, "rlu_moe_gemm_split")
+
+    # -- _act_quant: fused silu-and-mul + group-128 quant --------------------------------------
+    def _act_quant(self):
+        ops.silu_mul_quant(self.ic1, group=ops.GROUP, out=(self.q2, self.s2))
+
+    def apply(self, output: torch.Tensor, hidden_states: torch.Tensor, topk_weights: torch.Tensor,
+              topk_ids: torch.Tensor, gather: bool = True,
+              side: torch.cuda.Stream | None = None) -> None:
+        """_apply_split: output [M, H] bf16 <- hidden_states [M, H] bf16 routed by topk_ids /
+        topk_weights [M, top_k]."""
+        M = hidden_states.shape[0]
+        assert M == self.M and topk_ids.shape == (M, self.top_k)
+        waited = self._lru_step_fused(topk_ids, gather, side)
+        ops.fp8_quant_group(hidden_states, ops.GROUP, out=(self.qx, self.xs))
+        if waited is not None:
+            torch.cuda.current_stream().wait_stream(waited)
+        self._gemm_split(self.ic1, self.qx, self.xs, self.slots.w13, self.slots.s13,
+                         self.full_ptrs[0], self.full_ptrs[1], None, self.top_k, self.npw1)
+        self._act_quant()
+        tw = topk_weights.reshape(-1)
+        if tw.dtype != torch.float32 or not tw.is_contiguous():   # as fused_topk already gives
+            self.tw.copy_(tw)
+            tw = self.tw
+        self._gemm_split(self.ic3, self.q2, self.s2, self.slots.w2, self.slots.s2,
+                         self.full_ptrs[2], self.full_ptrs[3], tw, 1, self.npw2)
+        ops.moe_sum(self.ic3.view(M, self.top_k, self.H), output)

@@ -183,14 +183,15 @@ class _Lazy:
         return (max(self.d) + 1,) + self.d[k].shape
 
 
-def run_gemm(ops, y, qx, xs, wq, ws, align, tw, mtk, top_k, npw=4, wv=0):
+def run_gemm(ops, y, qx, xs, wq, ws, align, tw, mtk, top_k, npw=4, wv=0, sk=0):
     s, e, n = align
-    ops._r4d_fp8_moe_gemm_into(y, qx, xs, wq, ws, None, s, e, n, tw, mtk, top_k, wv, 1, npw)
+    ops._r4d_fp8_moe_gemm_into(y, qx, xs, wq, ws, None, s, e, n, tw, mtk, top_k, wv, sk, npw)
 
 
+@pytest.mark.parametrize("sk", [0, 1, 2, 4])
 @pytest.mark.parametrize("npw", [1, 2, 4, 8])
 @pytest.mark.parametrize("M", [1, 5, 20])
-def test_moe_gemm1_vs_oracle(ops, layer, npw, M):
+def test_moe_gemm1_vs_oracle(ops, layer, npw, M, sk):
     E, H, I = layer["E"], layer["H"], layer["I"]
     top_k = 10
     ids = routing(M, top_k, E, seed=M)
@@ -205,9 +206,9 @@ def test_moe_gemm1_vs_oracle(ops, layer, npw, M):
     y = torch.full((mtk, 2 * I), float("nan"), dtype=torch.bfloat16, device=DEV)
     qx_t = torch.from_numpy(qx).to(DEV).view(torch.float8_e4m3fn)
     xs_t = torch.from_numpy(xs).to(DEV)
-    gpu_case(f"moe gemm1 M={M} npw={npw}")
+    gpu_case(f"moe gemm1 M={M} npw={npw} sk={sk}")
     run_gemm(ops, y, qx_t, xs_t, layer["w13q"], layer["w13s"], to_dev_i32(*al), None, mtk,
-             top_k, npw=npw)
+             top_k, npw=npw, sk=sk)
     torch.cuda.synchronize()
     got = np_from_bf16(y)
     assert not np.isnan(got).any()
@@ -215,9 +216,10 @@ def test_moe_gemm1_vs_oracle(ops, layer, npw, M):
     assert err <= TOL, f"rel err {err:.3e}"
 
 
+@pytest.mark.parametrize("sk", [0, 1, 2])
 @pytest.mark.parametrize("npw", [1, 4])
 @pytest.mark.parametrize("M", [1, 5, 20])
-def test_moe_gemm2_routed_weight_vs_oracle(ops, layer, npw, M):
+def test_moe_gemm2_routed_weight_vs_oracle(ops, layer, npw, M, sk):
     E, H, I = layer["E"], layer["H"], layer["I"]
     top_k = 10
     ids = routing(M, top_k, E, seed=M + 7)
@@ -231,10 +233,10 @@ def test_moe_gemm2_routed_weight_vs_oracle(ops, layer, npw, M):
     wq, ws = ref_from(layer["w2q"], layer["w2s"], used)
     want = ogemm.moe_gemm(q2, s2, _Lazy(wq), _Lazy(ws), *al, mtk, 1, tw=tw)
     y = torch.full((mtk, H), float("nan"), dtype=torch.bfloat16, device=DEV)
-    gpu_case(f"moe gemm2 M={M} npw={npw}")
+    gpu_case(f"moe gemm2 M={M} npw={npw} sk={sk}")
     run_gemm(ops, y, torch.from_numpy(q2).to(DEV).view(torch.float8_e4m3fn),
              torch.from_numpy(s2).to(DEV), layer["w2q"], layer["w2s"], to_dev_i32(*al),
-             torch.from_numpy(tw).to(DEV), mtk, 1, npw=npw)
+             torch.from_numpy(tw).to(DEV), mtk, 1, npw=npw, sk=sk)
     torch.cuda.synchronize()
     err = ogemm.rel_err(np_from_bf16(y), want)
     assert err <= TOL, f"rel err {err:.3e}"
@@ -347,7 +349,8 @@ def test_moe_gemm_return_codes(ops, layer):
     q = torch.zeros((1, 2560), dtype=torch.float8_e4m3fn, device=DEV)
     s = torch.zeros((1, 20), dtype=torch.float32, device=DEV)
     al = to_dev_i32(np.zeros(16), np.zeros(1), np.zeros(1))
-    for wv, sk, npw, want in ((0, 2, 4, -4), (0, 1, 3, -6), (17, 1, 4, -5)):
+    # sk 3 does not divide K/128 = 20, sk 5 is not a supported split
+    for wv, sk, npw, want in ((0, 3, 4, -4), (0, 5, 4, -4), (0, 1, 3, -6), (17, 1, 4, -5)):
         with pytest.raises(RuntimeError, match=f"rc={want}"):
             ops._r4d_fp8_moe_gemm_into(y, q, s, layer["w13q"], layer["w13s"], None, *al, None,
                                        10, 10, wv, sk, npw)
@@ -387,3 +390,44 @@ def test_fp8_lmhead_vs_dequant_reference(ops, lm_head, M):
         if am[r] != ar[r]:
             gap = (ref[r, ar[r]] - ref[r, am[r]]).abs().item()
             assert gap <= 2 ** -7 * ref[r, ar[r]].abs().item(), (r, gap)
+
+
+def test_moe_gemm_split_one_launch_equals_two_calls(pkg, ops, layer):
+    """rlu_moe_gemm_split (hot slots + full tensor in one launch) == the two reference-style
+    calls, bit for bit, with the full tensor in pinned host memory read over PCIe."""
+    E, H, I = layer["E"], layer["H"], layer["I"]
+    M, top_k = 5, 10
+    ids = routing(M, top_k, E, seed=41)
+    mtk = ids.size
+    hot_experts = sorted(set(ids.reshape(-1).tolist()))[1::2]
+    hot = {ex: i for i, ex in enumerate(hot_experts)}
+    al = to_dev_i32(*align_all(ids, E, hot))
+    idx = torch.tensor(hot_experts, device=DEV)
+    sq, ss = layer["w13q"][idx].contiguous(), layer["w13s"][idx].contiguous()
+    hq = torch.empty(layer["w13q"].shape, dtype=layer["w13q"].dtype, pin_memory=True)
+    hs = torch.empty(layer["w13s"].shape, dtype=torch.float32, pin_memory=True)
+    hq.copy_(layer["w13q"])
+    hs.copy_(layer["w13s"])
+    from importlib import import_module
+    moe = import_module(pkg.__name__ + ".moe")
+    hqp, hsp = moe.device_ptr_of_pinned(hq), moe.device_ptr_of_pinned(hs)
+    x = fp8.bf16_round(np.random.default_rng(3).standard_normal((M, H)).astype(np.float32))
+    qx, xs = fp8.group_quant(x, 128)
+    qx_t = torch.from_numpy(qx).to(DEV).view(torch.float8_e4m3fn)
+    xs_t = torch.from_numpy(xs).to(DEV)
+    y2 = torch.full((mtk, 2 * I), float("nan"), dtype=torch.bfloat16, device=DEV)
+    gpu_case("split gemm: two calls")
+    run_gemm(ops, y2, qx_t, xs_t, sq, ss, al[0:3], None, mtk, top_k)
+    run_gemm(ops, y2, qx_t, xs_t, layer["w13q"], layer["w13s"], al[3:6], None, mtk, top_k)
+    y1 = torch.full_like(y2, float("nan"))
+    P = ctypes.c_void_p
+    gpu_case("split gemm: one launch, cold side from pinned host memory")
+    rc = pkg.lib().rlu_moe_gemm_split(
+        P(qx_t.data_ptr()), P(xs_t.data_ptr()), P(sq.data_ptr()), P(ss.data_ptr()),
+        P(al[0].data_ptr()), P(al[1].data_ptr()), P(al[2].data_ptr()), P(hqp), P(hsp),
+        P(al[3].data_ptr()), P(al[4].data_ptr()), P(al[5].data_ptr()), P(0), P(y1.data_ptr()),
+        al[0].numel(), mtk, top_k, H, 2 * I, 0, 4, P(torch.cuda.current_stream().cuda_stream))
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert not torch.isnan(y1).any()
+    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
