@@ -55,8 +55,9 @@ def log(msg):
 
 
 # ---- workload ---------------------------------------------------------------------------------
-def make_pool(torch, dev):
-    """512 experts, fp8 + block scales, quantized on the GPU (chunks of 32 experts)."""
+def make_pool(torch, dev, ops):
+    """512 experts, fp8 + block scales, quantized on the GPU (chunks of 32 experts) and stored
+    in the fragment order the GEMMs read."""
     def quant(w):
         n, k = w.shape[-2], w.shape[-1]
         b = w.reshape(w.shape[0], n // 128, 128, k // 128, 128)
@@ -70,7 +71,7 @@ def make_pool(torch, dev):
         ws = torch.empty((E, n // 128, k // 128), dtype=torch.float32, device=dev)
         for e0 in range(0, E, 32):
             q, s = quant(torch.randn(32, n, k, device=dev, generator=g) * 0.02)
-            wq[e0:e0 + 32] = q
+            ops.shuffle_fp8_weight(q.contiguous(), out=wq[e0:e0 + 32])
             ws[e0:e0 + 32] = s
         out[name], out[name + "s"] = wq, ws
     return out
@@ -173,9 +174,9 @@ def gemm_roofline(torch, pkg, layers, ids_last, rows, reps=3):
     def launches():
         for L in layers:
             L._gemm_split(L.ic1, L.qx, L.xs, L.slots.w13, L.slots.s13, L.full_ptrs[0],
-                          L.full_ptrs[1], None, L.top_k, L.npw1)
+                          L.full_ptrs[1], None, L.top_k, L.npw1, L.sk1)
             L._gemm_split(L.ic3, L.q2, L.s2, L.slots.w2, L.slots.s2, L.full_ptrs[2],
-                          L.full_ptrs[3], L.tw, 1, L.npw2)
+                          L.full_ptrs[3], L.tw, 1, L.npw2, L.sk2)
     launches()
     torch.cuda.synchronize()
     best = 1e30
@@ -189,7 +190,8 @@ def gemm_roofline(torch, pkg, layers, ids_last, rows, reps=3):
     gbs = per_launch_bytes / (best * 1e-6) / 1e9
     return dict(bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s",
                 frac=round(gbs / HBM_PEAK_GBS, 4), traffic=None,
-                kernel="rlu::moe_gemm_k<4, false> (gate_up and down, hot+cold in one launch)",
+                kernel=f"rlu::moe_gemm_k (gate_up npw {layers[0].npw1} sk {layers[0].sk1}, down "
+                       f"npw {layers[0].npw2} sk {layers[0].sk2}; hot + cold in one launch)",
                 avg_launch_us=round(best, 2), algorithmic_bytes_per_launch=int(per_launch_bytes),
                 distinct_experts_per_layer=round(float(d.mean()), 1))
 
@@ -299,7 +301,7 @@ def main():
     torch.cuda.set_device(dev)
     t_setup = time.perf_counter()
     log("generating 512 fp8 experts")
-    pool = make_pool(torch, dev)
+    pool = make_pool(torch, dev, pkg.ops)
     host = {n: torch.empty(t.shape, dtype=t.dtype, pin_memory=True) for n, t in pool.items()}
     for n in pool:
         host[n].copy_(pool[n])

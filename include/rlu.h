@@ -88,12 +88,14 @@ int rlu_moe_sum(const void* in, int M, int top_k, int H, void* out, hipStream_t 
  * Replaces the closed r4d_gemm_moe_mxfp4a8_nt_b16 behind the op r4d_mxfp4_moe_gemm_into
  * (patches/.../r4d_mxfp4_moe.py.lru.diff:363-395; argument order of
  * tests/k1/moe_ref_harness.py:55-56,221-226), for e4m3 weights with 128x128 float32 block scales:
- *   qx [mtk/top_k, K] e4m3, xs [mtk/top_k, K/128] f32, wq [E, N, K] e4m3, ws [E, N/128, K/128]
+ *   qx [mtk/top_k, K] e4m3, xs [mtk/top_k, K/128] f32, wq [E, N, K] e4m3 in fragment order
+ *   (rlu_shuffle_fp8_weight; the closed kernel likewise took pre-shuffled weights), ws [E, N/128, K/128]
  *   f32, wref unused (the reference's second scale slot), y [mtk, N] bf16, sorted_ids [em],
  *   expert_ids [em/16], num_post_pad [1] (read on the device), topk_weights [mtk] f32 or null.
  * Row contract of the reference kernel: sorted ids >= mtk are padding, expert id -1 skips the
  * block, only named rows are written, y[row] *= topk_weights[row] when given.
- * wv = workgroups per CU of the persistent grid (0: 3), sk = waves of a workgroup that split
+ * wv = workgroups per CU of a persistent grid (0: one workgroup per item group, balanced by the
+ * hardware dispatcher), sk = waves of a workgroup that split
  * one tile's K range (1, 2, 4; 0: the largest that divides K/128), npw = 16-column tiles per
  * item (1, 2, 4, 8). Partial sums are added in a fixed order, so a given sk is deterministic.
  * Returns -1 bad sizes, -2 K or N not a multiple of 128, -4 sk unsupported or not dividing
@@ -109,19 +111,28 @@ int r4d_gemm_moe_fp8blk_nt_b16(const void* qx, const float* xs, const void* wq,
  * _gemm_split (patches/.../r4d_mxfp4_moe.py.lru.diff:584-592) -- resident slots, then the full
  * expert tensor -- in one launch. Block list 1 (sorted_hot, eids_hot, npad_hot, em entries)
  * runs against wq_hot / ws_hot, block list 2 against wq / ws (device or pinned host memory).
- * Same row contract, checks and codes as r4d_gemm_moe_fp8blk_nt_b16 with sk = 0, so its output
- * equals the two sk = 0 calls bit for bit. */
+ * Same row contract, arguments, checks and codes as r4d_gemm_moe_fp8blk_nt_b16, so its output
+ * equals the two calls with the same sk bit for bit. */
 int rlu_moe_gemm_split(const void* qx, const float* xs, const void* wq_hot, const float* ws_hot,
                        const int* sorted_hot, const int* eids_hot, const int* npad_hot,
                        const void* wq, const float* ws, const int* sorted_cold,
                        const int* eids_cold, const int* npad_cold, const float* topk_weights,
-                       void* y, int em, int mtk, int top_k, int K, int N, int wv, int npw,
-                       hipStream_t stream);
+                       void* y, int em, int mtk, int top_k, int K, int N, int wv, int sk,
+                       int npw, hipStream_t stream);
 
 /* Replaces fp8hip_gemm_w8a8_launch behind gemm_fp8_block (kernels/fp8_target_lmhead.py:70-74):
- * y [M, N] bf16 = qx [M, K] (xs [M, K/128]) x w [N, K] (ws [N/128, K/128])^T, 1 <= M <= 16. */
+ * y [M, N] bf16 = qx [M, K] (xs [M, K/128]) x w [N, K] (ws [N/128, K/128])^T, 1 <= M <= 16,
+ * w in fragment order (rlu_shuffle_fp8_weight), as fp8hip takes shuffle_weight_gfx1201 output. */
 int rlu_gemm_fp8blk_m16(const void* qx, const float* xs, const void* w, const float* ws,
                         void* y, int M, int N, int K, int wv, int npw, hipStream_t stream);
+
+/* Replaces shuffle_weight_gfx1201 (the load-time weight shuffle behind pack_fp8_block,
+ * kernels/fp8_target_lmhead.py:44-66) for gfx950: row-major e4m3 [rows, K] -> MFMA fragment
+ * order, the layout every GEMM above reads. Byte (n, k), n = 16 nt + r,
+ * k = 128 kb + 64 h + 16 c + j, lands at ((nt (K/128) + kb) 2 + h) 1024 + (16 c + r) 16 + j:
+ * a permutation inside each 16-row strip, so stacked experts [E, N, K] shuffle as rows = E N.
+ * rows % 16 == 0, K % 128 == 0, out must not overlap w. Returns -1 / -2 on bad sizes. */
+int rlu_shuffle_fp8_weight(const void* w, void* out, long long rows, int K, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -25,6 +25,12 @@ Functions and what pins them (tests/test_oracle_quant.py):
                     the convention of this path, documented and pinned by its own fixtures.
   block_quant_weight()  kernels/fp8_target_lmhead.py:57-64: per 128x128 block, scale =
                     clamp(amax, 1e-12) / 448, wq = e4m3(clamp(w / scale, +-448)).
+  shuffle_weight() / unshuffle_weight()  the gfx950 MFMA fragment order of the weight bytes
+                    (the counterpart of shuffle_weight_gfx1201, kernels/fp8_target_lmhead.py:
+                    47,64): byte (n, k), n = 16 nt + r, k = 128 kb + 64 h + 16 c + j, at
+                    ((nt (K/128) + kb) 2 + h) 1024 + (16 c + r) 16 + j. Pinned by a brute-force
+                    walk of that formula over every byte (as tests/k3/test_layout.py:1-31 pins
+                    the gfx1201 layout) and by unshuffle(shuffle(w)) == w.
 """
 from __future__ import annotations
 
@@ -201,3 +207,20 @@ def dequant_act(q: np.ndarray, scale: np.ndarray) -> np.ndarray:
     v = e4m3_to_f32(q)
     gs = v.shape[1] // scale.shape[1]
     return v * np.repeat(scale, gs, 1)
+
+
+def shuffle_weight(w: np.ndarray) -> np.ndarray:
+    """uint8 [..., N, K] row-major -> the same shape in fragment order."""
+    *lead, N, K = w.shape
+    assert N % 16 == 0 and K % 128 == 0
+    v = np.ascontiguousarray(w).reshape(-1, N // 16, 16, K // 128, 2, 4, 16)
+    # (e, nt, r, kb, h, c, j) -> (e, nt, kb, h, c, r, j)
+    return np.ascontiguousarray(v.transpose(0, 1, 3, 4, 5, 2, 6)).reshape(w.shape)
+
+
+def unshuffle_weight(s: np.ndarray) -> np.ndarray:
+    """Inverse of shuffle_weight."""
+    *lead, N, K = s.shape
+    v = np.ascontiguousarray(s).reshape(-1, N // 16, K // 128, 2, 4, 16, 16)
+    # (e, nt, kb, h, c, r, j) -> (e, nt, r, kb, h, c, j)
+    return np.ascontiguousarray(v.transpose(0, 1, 5, 2, 3, 4, 6)).reshape(s.shape)

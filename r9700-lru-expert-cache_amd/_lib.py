@@ -16,6 +16,7 @@ LIB_PATH = pathlib.Path(os.environ.get(
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 _L = ctypes.c_long
+_LL = ctypes.c_longlong
 
 # name -> (restype, argtypes); one line per export of include/rlu.h
 SIGNATURES: dict[str, tuple] = {
@@ -27,7 +28,8 @@ SIGNATURES: dict[str, tuple] = {
     "rlu_moe_sum": (_I, [_P, _I, _I, _I, _P, _P]),
     "r4d_gemm_moe_fp8blk_nt_b16": (_I, [_P] * 10 + [_I] * 8 + [_P]),
     "rlu_gemm_fp8blk_m16": (_I, [_P] * 5 + [_I] * 5 + [_P]),
-    "rlu_moe_gemm_split": (_I, [_P] * 14 + [_I] * 7 + [_P]),
+    "rlu_moe_gemm_split": (_I, [_P] * 14 + [_I] * 8 + [_P]),
+    "rlu_shuffle_fp8_weight": (_I, [_P, _P, _LL, _I, _P]),
 }
 
 

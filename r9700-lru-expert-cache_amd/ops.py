@@ -9,6 +9,9 @@ Mirrors the reference's Python entry points for these stages:
                                   363-423), same argument list; ws_t = [E, N/128, K/128] fp32
                                   block scales, x_scale = [rows, K/128]; wref unused
   gemm_fp8_block                  kernels/fp8_target_lmhead.py:70-74
+  shuffle_fp8_weight              shuffle_weight_gfx1201 (kernels/fp8_target_lmhead.py:47,64),
+                                  here the gfx950 MFMA fragment order every GEMM reads
+  pack_fp8_block                  kernels/fp8_target_lmhead.py:44-66
 Errors from the C-ABI raise RuntimeError; there is no fallback implementation.
 """
 from __future__ import annotations
@@ -118,3 +121,36 @@ def gemm_fp8_block(x: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor) -> torch
     (kernels/fp8_target_lmhead.py:70-74); M <= 16."""
     qx, xs = fp8_quant_group(x.contiguous(), GROUP)
     return gemm_fp8_block_q(qx, xs, wq, ws)
+
+
+def shuffle_fp8_weight(w: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Row-major e4m3 [..., N, K] -> the same shape in gfx950 fragment order (a permutation
+    inside each 16-row strip; stacked experts shuffle as one [E*N, K] matrix)."""
+    assert w.dtype == FP8 and w.is_cuda and w.is_contiguous() and w.ndim >= 2
+    K = w.shape[-1]
+    rows = w.numel() // K
+    o = torch.empty_like(w) if out is None else out
+    assert o.shape == w.shape and o.dtype == FP8 and o.is_contiguous()
+    assert o.data_ptr() != w.data_ptr(), "shuffle is out of place"
+    rc = lib().rlu_shuffle_fp8_weight(_p(w), _p(o), rows, K, _P(stream_ptr()))
+    check(rc, "rlu_shuffle_fp8_weight")
+    return o
+
+
+@torch.no_grad()
+def pack_fp8_block(w: torch.Tensor, rows: int = 4096) -> tuple[torch.Tensor, torch.Tensor]:
+    """bf16/fp32 [N, K] -> (e4m3 [N, K] in fragment order, fp32 block scales [N/128, K/128]):
+    per 128x128 block scale = max(amax, 1e-12) / 448, q = e4m3(clamp(w / scale, +-448))
+    (kernels/fp8_target_lmhead.py:44-66), quantized in row chunks so the fp32 temporaries stay
+    small."""
+    N, K = w.shape
+    assert N % 128 == 0 and K % 128 == 0, (N, K)
+    q = torch.empty((N, K), dtype=FP8, device=w.device)
+    ws = torch.empty((N // 128, K // 128), dtype=torch.float32, device=w.device)
+    for r0 in range(0, N, rows):
+        r1 = min(N, r0 + rows)
+        wf = w[r0:r1].float().view((r1 - r0) // 128, 128, K // 128, 128)
+        scale = wf.abs().amax(dim=(1, 3), keepdim=True).clamp(min=1e-12) / 448.0
+        q[r0:r1] = (wf / scale).clamp(-448.0, 448.0).to(FP8).view(r1 - r0, K)
+        ws[r0 // 128:r1 // 128] = scale.view((r1 - r0) // 128, K // 128)
+    return shuffle_fp8_weight(q), ws

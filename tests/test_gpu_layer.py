@@ -1,0 +1,117 @@
+"""GPU: LruMoELayer.apply (the _apply_split path, r4d_mxfp4_moe.py.lru.diff:659-696) end to end
+against the oracle pipeline, over consecutive decode steps of Zipf routing with misses.
+
+Per step:
+* the cache state after the step equals oracle.lru.fused's, bit for bit (table, map_cold,
+  slot_expert, slot_stamp, step, miss, n_miss);
+* residency: after the side-stream gather every slot holds the bytes of the expert its
+  slot_expert entry names, in all four per-expert buffers (w13, s13, w2, s2);
+* the layer output is within 2e-2 of max|ref| of the oracle pipeline: group-128 quant, float64
+  gate_up GEMM over the row-major weights, bf16, SiLU-mul-quant, float64 down GEMM x routed
+  weights, bf16, moe_sum -- computed with every expert resident (the hot/cold partition must not
+  change the result).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import gpu_case
+from oracle import fp8, gemm as ogemm
+from oracle import lru as olru
+from oracle import trace
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TOL = 2e-2
+E, S, H, I, TOPK = 128, 100, 2560, 768, 10   # read-through above 50 distinct
+
+
+@pytest.fixture(scope="module")
+def ops(pkg):
+    from importlib import import_module
+    return import_module(pkg.__name__ + ".ops")
+
+
+@pytest.fixture(scope="module")
+def pool(pkg, ops):
+    """E experts: row-major e4m3 copies for the oracle, fragment-order pinned host copies for
+    the layer (the gather source and the cold GEMM operand)."""
+    g = torch.Generator(device=DEV).manual_seed(7)
+    out = {}
+    for name, (n, k) in (("w13", (2 * I, H)), ("w2", (H, I))):
+        w = torch.randn(E, n, k, device=DEV, generator=g) * 0.02
+        b = w.reshape(E, n // 128, 128, k // 128, 128)
+        ws = (b.abs().amax(dim=(2, 4)).clamp(min=1e-12) / 448.0).float()
+        wq = (b / ws[:, :, None, :, None]).clamp(-448, 448).to(torch.float8_e4m3fn).reshape(E, n, k)
+        del w, b
+        out[name + "_np"] = wq.view(torch.uint8).cpu().numpy()
+        out[name + "s_np"] = ws.cpu().numpy()
+        t = ops.shuffle_fp8_weight(wq.contiguous())
+        h = torch.empty(t.shape, dtype=t.dtype, pin_memory=True)
+        h.copy_(t)
+        hs = torch.empty(ws.shape, dtype=torch.float32, pin_memory=True)
+        hs.copy_(ws)
+        out[name], out[name + "s"] = h, hs
+    return out
+
+
+def oracle_layer(x, ids, tw, pool):
+    """The pipeline of apply() on the CPU with every expert resident."""
+    M = x.shape[0]
+    mtk = ids.size
+    L, NB = olru.align_sizes(mtk, E, 16)
+    s, e, n = olru.align(ids.reshape(-1), E, E, np.arange(E, dtype=np.int32), 16, L, NB)[:3]
+    qx, xs = fp8.group_quant(x, 128)
+    y1 = ogemm.moe_gemm(qx, xs, pool["w13_np"], pool["w13s_np"], s, e, n, mtk, TOPK)
+    _, q2, s2 = fp8.silu_mul_quant(fp8.bf16_round(y1.astype(np.float32)), 128)
+    y2 = ogemm.moe_gemm(q2, s2, pool["w2_np"], pool["w2s_np"], s, e, n, mtk, 1,
+                        tw=tw.reshape(-1))
+    return ogemm.moe_sum(fp8.bf16_round(y2.astype(np.float32)), M, TOPK)
+
+
+@pytest.mark.parametrize("M", [5, 20])
+def test_layer_steps_vs_oracle(pkg, pool, M):
+    steps = 4
+    tr, perm0 = trace.zipf_trace(seed=300 + M, E=E, rows=M, k=TOPK, steps=steps, s=1.1,
+                                 corr=0.7 if M >= 20 else 0.0)
+    ids_all = tr.reshape(steps, M, TOPK).astype(np.int32)
+    hot, rank = trace.warm_hot(perm0, S)
+    full = pkg.ExpertWeights(pool["w13"], pool["w13s"], pool["w2"], pool["w2s"])
+    layer = pkg.LruMoELayer(full, hot, rank, M, TOPK, DEV)
+    st = olru.warm_start(E, S, hot, rank)
+    rng = np.random.default_rng(M)
+    side = torch.cuda.Stream()
+    total_miss = 0
+    for t in range(steps):
+        ids = ids_all[t]
+        x = fp8.bf16_round(rng.standard_normal((M, H)).astype(np.float32))
+        tw = rng.random((M, TOPK)).astype(np.float32)
+        out = torch.empty((M, H), dtype=torch.bfloat16, device=DEV)
+        gpu_case(f"layer M={M} step {t}")
+        layer.apply(out, torch.from_numpy(x).to(torch.bfloat16).to(DEV),
+                    torch.from_numpy(tw).to(DEV), torch.from_numpy(ids).to(DEV),
+                    gather=True, side=side)
+        torch.cuda.synchronize()
+        olru.fused(st, ids.reshape(-1), 16)
+        for name, got in zip(olru.LruState.NAMES, layer.cache.state()):
+            if name == "routed":
+                continue
+            assert np.array_equal(got.cpu().numpy(), getattr(st, name)), (t, name)
+        total_miss += int(st.n_miss[0])
+        # residency: slot s holds slot_expert[s]'s bytes in all four buffers
+        se = st.slot_expert
+        live = np.nonzero(se >= 0)[0]
+        idx = torch.from_numpy(se[live].astype(np.int64))
+        for name in ("w13", "w13s", "w2", "w2s"):
+            src = pool[name].index_select(0, idx)
+            dst = getattr(layer.slots, {"w13": "w13", "w13s": "s13", "w2": "w2",
+                                        "w2s": "s2"}[name])[torch.from_numpy(live).to(DEV)]
+            assert torch.equal(src.view(torch.uint8).reshape(len(live), -1),
+                               dst.cpu().view(torch.uint8).reshape(len(live), -1)), (t, name)
+        ref = oracle_layer(x, ids, tw, pool)
+        got = out.float().cpu().numpy()
+        err = ogemm.rel_err(got, ref)
+        assert err <= TOL, f"step {t}: rel err {err:.3e}"
+    assert total_miss > 0, "the trace must exercise the miss path"

@@ -9,7 +9,9 @@
   read on the device; partition invariance (hot call + cold call == one call, bit-identical,
   tests/lru/test_numerics_lru.py:183-198); HIP-graph replay == eager;
 * fp8 lm_head GEMM at 151936 x 2560: within tolerance and argmax equal to the fp32-dequant
-  reference's.
+  reference's;
+* the fragment-order weight shuffle: bit-exact against the oracle's; the kernels read shuffled
+  weights, the oracle the row-major ones, so every GEMM test also checks the layout end to end.
 """
 from __future__ import annotations
 
@@ -155,12 +157,35 @@ def to_dev_i32(*arrs):
 
 
 @pytest.fixture(scope="module")
-def layer():
-    """One MoE layer at the real expert shapes, 40 experts."""
+def layer(ops):
+    """One MoE layer at the real expert shapes, 40 experts: row-major weights for the oracle
+    (w13q, w2q) and their fragment-order shuffles for the kernels (w13t, w2t)."""
     E, H, I = 40, 2560, 768
     w13q, w13s = make_experts(E, 2 * I, H, 2)
     w2q, w2s = make_experts(E, H, I, 3)
-    return dict(E=E, H=H, I=I, w13q=w13q, w13s=w13s, w2q=w2q, w2s=w2s)
+    return dict(E=E, H=H, I=I, w13q=w13q, w13s=w13s, w2q=w2q, w2s=w2s,
+                w13t=ops.shuffle_fp8_weight(w13q), w2t=ops.shuffle_fp8_weight(w2q))
+
+
+@pytest.mark.parametrize("shape", [(1, 16, 128), (3, 48, 384), (40, 1536, 2560)])
+def test_shuffle_kernel_matches_oracle(ops, shape):
+    g = torch.Generator(device=DEV).manual_seed(sum(shape))
+    w = torch.randint(0, 256, shape, dtype=torch.uint8, device=DEV, generator=g)
+    w = w.view(torch.float8_e4m3fn)
+    gpu_case(f"shuffle {shape}")
+    got = u8(ops.shuffle_fp8_weight(w))
+    assert np.array_equal(got, fp8.shuffle_weight(u8(w)))
+    assert np.array_equal(fp8.unshuffle_weight(got), u8(w))
+
+
+def test_shuffle_return_codes(pkg):
+    P = ctypes.c_void_p
+    x = torch.empty(4096, dtype=torch.uint8, device=DEV)
+    o = torch.empty_like(x)
+    s = P(torch.cuda.current_stream().cuda_stream)
+    assert pkg.lib().rlu_shuffle_fp8_weight(P(x.data_ptr()), P(o.data_ptr()), 0, 128, s) == -1
+    assert pkg.lib().rlu_shuffle_fp8_weight(P(x.data_ptr()), P(o.data_ptr()), 8, 128, s) == -2
+    assert pkg.lib().rlu_shuffle_fp8_weight(P(x.data_ptr()), P(o.data_ptr()), 16, 64, s) == -2
 
 
 def ref_from(dev_wq, dev_ws, experts):
@@ -207,7 +232,7 @@ def test_moe_gemm1_vs_oracle(ops, layer, npw, M, sk):
     qx_t = torch.from_numpy(qx).to(DEV).view(torch.float8_e4m3fn)
     xs_t = torch.from_numpy(xs).to(DEV)
     gpu_case(f"moe gemm1 M={M} npw={npw} sk={sk}")
-    run_gemm(ops, y, qx_t, xs_t, layer["w13q"], layer["w13s"], to_dev_i32(*al), None, mtk,
+    run_gemm(ops, y, qx_t, xs_t, layer["w13t"], layer["w13s"], to_dev_i32(*al), None, mtk,
              top_k, npw=npw, sk=sk)
     torch.cuda.synchronize()
     got = np_from_bf16(y)
@@ -235,7 +260,7 @@ def test_moe_gemm2_routed_weight_vs_oracle(ops, layer, npw, M, sk):
     y = torch.full((mtk, H), float("nan"), dtype=torch.bfloat16, device=DEV)
     gpu_case(f"moe gemm2 M={M} npw={npw} sk={sk}")
     run_gemm(ops, y, torch.from_numpy(q2).to(DEV).view(torch.float8_e4m3fn),
-             torch.from_numpy(s2).to(DEV), layer["w2q"], layer["w2s"], to_dev_i32(*al),
+             torch.from_numpy(s2).to(DEV), layer["w2t"], layer["w2s"], to_dev_i32(*al),
              torch.from_numpy(tw).to(DEV), mtk, 1, npw=npw, sk=sk)
     torch.cuda.synchronize()
     err = ogemm.rel_err(np_from_bf16(y), want)
@@ -257,7 +282,7 @@ def test_moe_gemm_row_contract(ops, layer):
 
     def written(s_, e_, n_):
         y = torch.full((mtk, 2 * I), float("nan"), dtype=torch.bfloat16, device=DEV)
-        run_gemm(ops, y, qx_t, xs_t, layer["w13q"], layer["w13s"], to_dev_i32(s_, e_, n_), None,
+        run_gemm(ops, y, qx_t, xs_t, layer["w13t"], layer["w13s"], to_dev_i32(s_, e_, n_), None,
                  mtk, top_k)
         torch.cuda.synchronize()
         return ~torch.isnan(y).any(dim=1).cpu().numpy(), y
@@ -289,7 +314,7 @@ def test_moe_gemm_partition_invariance(ops, layer):
     hot_experts = sorted(set(ids.reshape(-1).tolist()))[::2]
     hot = {ex: i for i, ex in enumerate(hot_experts)}
     sh, eh, nh, sc, ec, nc = align_all(ids, E, hot)
-    slots_q = layer["w13q"][torch.tensor(hot_experts, device=DEV)].contiguous()
+    slots_q = layer["w13t"][torch.tensor(hot_experts, device=DEV)].contiguous()
     slots_s = layer["w13s"][torch.tensor(hot_experts, device=DEV)].contiguous()
     x = fp8.bf16_round(np.random.default_rng(2).standard_normal((M, H)).astype(np.float32))
     qx, xs = fp8.group_quant(x, 128)
@@ -298,10 +323,10 @@ def test_moe_gemm_partition_invariance(ops, layer):
     y = torch.full((mtk, 2 * I), float("nan"), dtype=torch.bfloat16, device=DEV)
     gpu_case("moe gemm partition invariance")
     run_gemm(ops, y, qx_t, xs_t, slots_q, slots_s, to_dev_i32(sh, eh, nh), None, mtk, top_k)
-    run_gemm(ops, y, qx_t, xs_t, layer["w13q"], layer["w13s"], to_dev_i32(sc, ec, nc), None,
+    run_gemm(ops, y, qx_t, xs_t, layer["w13t"], layer["w13s"], to_dev_i32(sc, ec, nc), None,
              mtk, top_k)
     y1 = torch.full_like(y, float("nan"))
-    run_gemm(ops, y1, qx_t, xs_t, layer["w13q"], layer["w13s"], to_dev_i32(*align_all(ids, E)),
+    run_gemm(ops, y1, qx_t, xs_t, layer["w13t"], layer["w13s"], to_dev_i32(*align_all(ids, E)),
              None, mtk, top_k)
     torch.cuda.synchronize()
     assert not torch.isnan(y).any()
@@ -327,19 +352,19 @@ def test_moe_gemm_graph_replay(ops, layer):
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
-        run_gemm(ops, y, qx_t, xs_t, layer["w13q"], layer["w13s"], al, None, mtk, top_k)
+        run_gemm(ops, y, qx_t, xs_t, layer["w13t"], layer["w13s"], al, None, mtk, top_k)
     torch.cuda.current_stream().wait_stream(side)
     g = torch.cuda.CUDAGraph()
     gpu_case("moe gemm graph capture")
     with torch.cuda.graph(g):
-        run_gemm(ops, y, qx_t, xs_t, layer["w13q"], layer["w13s"], al, None, mtk, top_k)
+        run_gemm(ops, y, qx_t, xs_t, layer["w13t"], layer["w13s"], al, None, mtk, top_k)
     for q, s_ in inputs:
         qx_t.copy_(q)
         xs_t.copy_(s_)
         g.replay()
         torch.cuda.synchronize()
         ye = torch.empty_like(y)
-        run_gemm(ops, ye, q, s_, layer["w13q"], layer["w13s"], al, None, mtk, top_k)
+        run_gemm(ops, ye, q, s_, layer["w13t"], layer["w13s"], al, None, mtk, top_k)
         torch.cuda.synchronize()
         assert torch.equal(y.view(torch.int16), ye.view(torch.int16))
 
@@ -352,30 +377,34 @@ def test_moe_gemm_return_codes(ops, layer):
     # sk 3 does not divide K/128 = 20, sk 5 is not a supported split
     for wv, sk, npw, want in ((0, 3, 4, -4), (0, 5, 4, -4), (0, 1, 3, -6), (17, 1, 4, -5)):
         with pytest.raises(RuntimeError, match=f"rc={want}"):
-            ops._r4d_fp8_moe_gemm_into(y, q, s, layer["w13q"], layer["w13s"], None, *al, None,
+            ops._r4d_fp8_moe_gemm_into(y, q, s, layer["w13t"], layer["w13s"], None, *al, None,
                                        10, 10, wv, sk, npw)
 
 
 # ---- fp8 lm_head -----------------------------------------------------------------------------
 @pytest.fixture(scope="module")
-def lm_head():
+def lm_head(ops):
     N, K = 151936, 2560
     g = torch.Generator(device=DEV).manual_seed(5)
     w = torch.randn(N, K, device=DEV, generator=g) * 0.02
     wq, ws = block_quant_gpu(w)
+    wt, ws2 = ops.pack_fp8_block(w)
     del w
-    return wq, ws
+    # pack_fp8_block is the same recipe as block_quant_gpu, then the shuffle
+    assert torch.equal(ws2, ws)
+    assert torch.equal(wt.view(torch.uint8), ops.shuffle_fp8_weight(wq).view(torch.uint8))
+    return wq, ws, wt
 
 
 @pytest.mark.parametrize("M", [1, 5, 8, 16])
 def test_fp8_lmhead_vs_dequant_reference(ops, lm_head, M):
-    wq, ws = lm_head
+    wq, ws, wt = lm_head
     N, K = wq.shape
     rng = np.random.default_rng(M + 4)
     x = fp8.bf16_round(rng.standard_normal((M, K)).astype(np.float32))
     xt = bf16_from_np(x)
     gpu_case(f"fp8 lm_head M={M}")
-    y = ops.gemm_fp8_block(xt, wq, ws)
+    y = ops.gemm_fp8_block(xt, wt, ws)
     torch.cuda.synchronize()
     qx, xs = fp8.group_quant(x, 128)
     a = torch.from_numpy(fp8.dequant_act(qx, xs)).to(DEV).double()
@@ -403,10 +432,10 @@ def test_moe_gemm_split_one_launch_equals_two_calls(pkg, ops, layer):
     hot = {ex: i for i, ex in enumerate(hot_experts)}
     al = to_dev_i32(*align_all(ids, E, hot))
     idx = torch.tensor(hot_experts, device=DEV)
-    sq, ss = layer["w13q"][idx].contiguous(), layer["w13s"][idx].contiguous()
-    hq = torch.empty(layer["w13q"].shape, dtype=layer["w13q"].dtype, pin_memory=True)
+    sq, ss = layer["w13t"][idx].contiguous(), layer["w13s"][idx].contiguous()
+    hq = torch.empty(layer["w13t"].shape, dtype=layer["w13t"].dtype, pin_memory=True)
     hs = torch.empty(layer["w13s"].shape, dtype=torch.float32, pin_memory=True)
-    hq.copy_(layer["w13q"])
+    hq.copy_(layer["w13t"])
     hs.copy_(layer["w13s"])
     from importlib import import_module
     moe = import_module(pkg.__name__ + ".moe")
@@ -418,7 +447,7 @@ def test_moe_gemm_split_one_launch_equals_two_calls(pkg, ops, layer):
     y2 = torch.full((mtk, 2 * I), float("nan"), dtype=torch.bfloat16, device=DEV)
     gpu_case("split gemm: two calls")
     run_gemm(ops, y2, qx_t, xs_t, sq, ss, al[0:3], None, mtk, top_k)
-    run_gemm(ops, y2, qx_t, xs_t, layer["w13q"], layer["w13s"], al[3:6], None, mtk, top_k)
+    run_gemm(ops, y2, qx_t, xs_t, layer["w13t"], layer["w13s"], al[3:6], None, mtk, top_k)
     y1 = torch.full_like(y2, float("nan"))
     P = ctypes.c_void_p
     gpu_case("split gemm: one launch, cold side from pinned host memory")
@@ -426,7 +455,8 @@ def test_moe_gemm_split_one_launch_equals_two_calls(pkg, ops, layer):
         P(qx_t.data_ptr()), P(xs_t.data_ptr()), P(sq.data_ptr()), P(ss.data_ptr()),
         P(al[0].data_ptr()), P(al[1].data_ptr()), P(al[2].data_ptr()), P(hqp), P(hsp),
         P(al[3].data_ptr()), P(al[4].data_ptr()), P(al[5].data_ptr()), P(0), P(y1.data_ptr()),
-        al[0].numel(), mtk, top_k, H, 2 * I, 0, 4, P(torch.cuda.current_stream().cuda_stream))
+        al[0].numel(), mtk, top_k, H, 2 * I, 0, 0, 4,
+        P(torch.cuda.current_stream().cuda_stream))
     assert rc == 0
     torch.cuda.synchronize()
     assert not torch.isnan(y1).any()

@@ -8,7 +8,8 @@
 * block weight quant against its closed form (kernels/fp8_target_lmhead.py:57-64);
 * the grouped-GEMM reference against a pure-Python triple loop on tiny shapes, including the
   row contract (padding rows, expert -1, num_post_pad);
-* moe_sum against a float64 sum within one bf16 rounding.
+* moe_sum against a float64 sum within one bf16 rounding;
+* the fragment-order weight shuffle against a byte-by-byte walk of its address formula.
 """
 from __future__ import annotations
 
@@ -144,3 +145,27 @@ def test_moe_sum_reference():
     want = x.astype(np.float64).reshape(5, 10, 64).sum(1)
     assert np.abs(out - want).max() <= np.abs(want).max() * 2 ** -7
     assert np.array_equal(out, fp8.bf16_round(out))
+
+
+def test_shuffle_layout_formula():
+    """Every byte (n, k) of a [2, 64, 384] stack lands where the fragment-order formula says
+    (the gfx950 counterpart of tests/k3/test_layout.py), and unshuffle inverts it."""
+    E, N, K = 2, 64, 384
+    w = (np.arange(E * N * K, dtype=np.int64) % 251).astype(np.uint8).reshape(E, N, K)
+    s = fp8.shuffle_weight(w)
+    flat = s.reshape(E, -1)
+    KB = K // 128
+    for e in range(E):
+        for n in range(N):
+            nt, r = divmod(n, 16)
+            for k in range(K):
+                kb, rem = divmod(k, 128)
+                h, rem = divmod(rem, 64)
+                c, j = divmod(rem, 16)
+                off = ((nt * KB + kb) * 2 + h) * 1024 + (16 * c + r) * 16 + j
+                assert flat[e, off] == w[e, n, k], (e, n, k)
+    assert np.array_equal(fp8.unshuffle_weight(s), w)
+    # the lane view: lane l = 16 c + r reads 16 contiguous bytes = row r, k in [16c, 16c + 16)
+    lane_bytes = s[0].reshape(-1)[:1024].reshape(64, 16)
+    for l in range(64):
+        assert np.array_equal(lane_bytes[l], w[0, l % 16, 16 * (l // 16):16 * (l // 16) + 16])
