@@ -78,7 +78,7 @@ def make_pool(torch, dev, ops):
 
 
 def layer_trace(layer, rows, steps):
-    from oracle import trace
+    trace = load_pkg().traces
     corr = 0.7 if rows >= 20 else 0.0
     return trace.zipf_trace(seed=1000 + layer, E=E, rows=rows, k=TOPK, steps=steps, s=1.1,
                             corr=corr)
@@ -86,7 +86,7 @@ def layer_trace(layer, rows, steps):
 
 def build(torch, pkg, rows, steps, dev, pool_dev, host_full, layers_cache=None):
     """Layers (slots shared between batch sizes: the hot set depends only on the layer seed)."""
-    from oracle import trace
+    trace = pkg.traces
     ids = np.empty((steps, LAYERS, rows, TOPK), np.int32)
     layers = []
     for l in range(LAYERS):
@@ -153,30 +153,51 @@ def distinct_per_layer(ids_step):
     return np.array([len(np.unique(ids_step[l])) for l in range(ids_step.shape[0])])
 
 
+def algorithmic_bytes(ids_last, rows):
+    """Bytes one grouped-GEMM launch must move, averaged over the 104 launches of a step: every
+    distinct expert's weights and block scales once, the activations and their scales once,
+    the output rows once (and the routed weights for the down projection)."""
+    mtk = rows * TOPK
+    total = 0.0
+    d = distinct_per_layer(ids_last)
+    for l in range(len(d)):
+        e = int(d[l])
+        total += (e * (2 * I * H + (2 * I // 128) * (H // 128) * 4)
+                  + rows * H + rows * (H // 128) * 4 + mtk * 2 * I * 2)        # gate_up
+        total += (e * (H * I + (H // 128) * (I // 128) * 4)
+                  + mtk * I + mtk * (I // 128) * 4 + mtk * H * 2 + mtk * 4)     # down
+    return total / (2 * len(d)), d
+
+
+def gemm_launches(layers):
+    """Both grouped GEMMs of every layer, eager, on the current stream (inputs as the last step
+    left them)."""
+    for L in layers:
+        L._gemm_split(L.ic1, L.qx, L.xs, L.slots.w13, L.slots.s13, L.full_ptrs[0],
+                      L.full_ptrs[1], None, L.top_k, L.npw1, L.sk1)
+        L._gemm_split(L.ic3, L.q2, L.s2, L.slots.w2, L.slots.s2, L.full_ptrs[2],
+                      L.full_ptrs[3], L.tw, 1, L.npw2, L.sk2)
+
+
+def load_traffic():
+    """HBM bytes per grouped-GEMM launch from the committed counter runs (FETCH_SIZE and
+    WRITE_SIZE of `bench.py --pmc-probe`, each scaled by the same counter on a plain copy of
+    known size), or None when the file is absent."""
+    p = ROOT / "profiles" / "moe_gemm_traffic_b4.json"
+    if not p.exists():
+        return None
+    return json.loads(p.read_text())
+
+
 def gemm_roofline(torch, pkg, layers, ids_last, rows, reps=3):
     """Average duration of the grouped GEMM launches of one step (both GEMMs of all 52 layers,
     eager, back to back on the current stream, HIP events around them) and the algorithmic
-    bytes each launch moves: every distinct expert's weights and scales once, the activations
-    and scales once, the output rows once."""
-    mtk = rows * TOPK
-    n = 0
-    bytes_total = 0.0
-    d = distinct_per_layer(ids_last)
-    for l, L in enumerate(layers):
-        e = int(d[l])
-        bytes_total += (e * (2 * I * H + (2 * I // 128) * (H // 128) * 4)
-                        + rows * H + rows * (H // 128) * 4 + mtk * 2 * I * 2)        # GEMM1
-        bytes_total += (e * (H * I + (H // 128) * (I // 128) * 4)
-                        + mtk * I + mtk * (I // 128) * 4 + mtk * H * 2 + mtk * 4)     # GEMM2
-        n += 2
-    per_launch_bytes = bytes_total / n
+    bytes each launch moves."""
+    per_launch_bytes, d = algorithmic_bytes(ids_last, rows)
+    n = 2 * len(layers)
 
     def launches():
-        for L in layers:
-            L._gemm_split(L.ic1, L.qx, L.xs, L.slots.w13, L.slots.s13, L.full_ptrs[0],
-                          L.full_ptrs[1], None, L.top_k, L.npw1, L.sk1)
-            L._gemm_split(L.ic3, L.q2, L.s2, L.slots.w2, L.slots.s2, L.full_ptrs[2],
-                          L.full_ptrs[3], L.tw, 1, L.npw2, L.sk2)
+        gemm_launches(layers)
     launches()
     torch.cuda.synchronize()
     best = 1e30
@@ -188,8 +209,11 @@ def gemm_roofline(torch, pkg, layers, ids_last, rows, reps=3):
         torch.cuda.synchronize()
         best = min(best, a.elapsed_time(b) * 1e3 / n)
     gbs = per_launch_bytes / (best * 1e-6) / 1e9
+    tr = load_traffic()
     return dict(bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s",
-                frac=round(gbs / HBM_PEAK_GBS, 4), traffic=None,
+                frac=round(gbs / HBM_PEAK_GBS, 4),
+                traffic=None if tr is None else tr["hbm_bytes_per_launch"],
+                traffic_source=None if tr is None else tr["source"],
                 kernel=f"rlu::moe_gemm_k (gate_up npw {layers[0].npw1} sk {layers[0].sk1}, down "
                        f"npw {layers[0].npw2} sk {layers[0].sk2}; hot + cold in one launch)",
                 avg_launch_us=round(best, 2), algorithmic_bytes_per_launch=int(per_launch_bytes),
@@ -218,6 +242,101 @@ def lru_us_per_layer(torch, layers, ids_dev, ids_static, t, reps=5):
     return best
 
 
+def lm_head_fp8(torch, pkg, dev, M=5, reps=20):
+    """The fp8 target lm_head GEMV: vocab 151936 x 2560 e4m3 in fragment order with 128x128
+    block scales (N(0, 0.02) weights, seed 5), x bf16 N(0, 1) [M, 2560] (seed 4), already
+    quantized per token group 128. Two weight copies alternate so that no launch finds its
+    389 MB in the 256 MB last-level cache. Bytes per launch: weights + scales + activations +
+    logits."""
+    N, K = 151936, 2560
+    ops = pkg.ops
+    g = torch.Generator(device=dev).manual_seed(5)
+    W = []
+    for _ in range(2):
+        w = torch.randn(N, K, device=dev, generator=g) * 0.02
+        W.append(ops.pack_fp8_block(w))
+        del w
+    torch.cuda.empty_cache()
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16).to(dev)
+    qx, xs = ops.fp8_quant_group(x)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    nbytes = N * K + (N // 128) * (K // 128) * 4 + M * K + M * (K // 128) * 4 + M * N * 2
+    for i in range(2):
+        ops.gemm_fp8_block_q(qx, xs, *W[i], out=y)
+    torch.cuda.synchronize()
+    best = 1e30
+    for _ in range(3):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for i in range(reps):
+            ops.gemm_fp8_block_q(qx, xs, *W[i % 2], out=y)
+        b.record()
+        torch.cuda.synchronize()
+        best = min(best, a.elapsed_time(b) * 1e3 / reps)
+    gbs = nbytes / (best * 1e-6) / 1e9
+    del W
+    torch.cuda.empty_cache()
+    return dict(M=M, us=round(best, 2), bytes=nbytes, achieved_gbs=round(gbs, 1),
+                frac=round(gbs / HBM_PEAK_GBS, 4))
+
+
+def lru_insert_sweep(torch, pkg, dev, reps=50, rounds=5):
+    """r4d_lru_fused time vs inserts per step at E=512, S=257 (the insert storm of
+    tests/lru/bench_victim.py:43-79): routing with exactly k non-resident experts among mk ids,
+    no read-through. Each graph replays (restore state, fused call) reps times; the restore
+    alone is timed the same way and subtracted."""
+    out = {}
+    for mk in (50, 200):
+        row = {}
+        for k in (0, 1, 2, 4, 8, 13, 14, 32, 64):
+            if k > mk - 10:                 # keep some resident experts in the step
+                continue
+            rng = np.random.default_rng(100 + k)
+            hot = np.sort(rng.choice(E, S, replace=False))
+            rank = {int(e): i for i, e in enumerate(rng.permutation(hot))}
+            cache = pkg.LruCache.build(E, hot, rank, dev)
+            cache.max_distinct = E
+            ids = torch.from_numpy(pkg.traces.insert_storm_ids(rng, hot, E, mk, k)).to(dev)
+            align = cache.alloc_align(mk)
+            pristine = [t.clone() for t in cache.state()]
+
+            def restore():
+                for t, v in zip(cache.state(), pristine):
+                    t.copy_(v)
+
+            def full():
+                restore()
+                cache.fused(ids, out=align)
+            times = {}
+            for name, fn in (("full", full), ("restore", restore)):
+                side = torch.cuda.Stream()
+                side.wait_stream(torch.cuda.current_stream())
+                with torch.cuda.stream(side):
+                    fn()
+                torch.cuda.current_stream().wait_stream(side)
+                torch.cuda.synchronize()
+                gr = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(gr):
+                    for _ in range(reps):
+                        fn()
+                gr.replay()
+                torch.cuda.synchronize()
+                best = 1e30
+                for _ in range(rounds):
+                    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    a.record()
+                    gr.replay()
+                    b.record()
+                    torch.cuda.synchronize()
+                    best = min(best, a.elapsed_time(b) * 1e3 / reps)
+                times[name] = best
+            nm = int(cache.n_miss.item())
+            assert nm == min(k, 64), (mk, k, nm)
+            row[str(k)] = round(times["full"] - times["restore"], 2)
+        out[f"mk{mk}"] = row
+    return out
+
+
 # ---- CPU baseline: the oracle restatement of one layer step, timed on the host ------------------
 def cpu_baseline(pool_cpu_w13, pool_cpu_w2, ids, budget_s=10.0):
     from oracle import fp8, lru as olru, gemm as ogemm
@@ -231,7 +350,7 @@ def cpu_baseline(pool_cpu_w13, pool_cpu_w2, ids, budget_s=10.0):
     rng = np.random.default_rng(1)
     x = fp8.bf16_round(rng.standard_normal((rows, H)).astype(np.float32))
     tw = rng.random(mtk).astype(np.float32)
-    from oracle import trace
+    trace = load_pkg().traces
     done = 0
     t0 = time.perf_counter()
     per = []
@@ -285,6 +404,10 @@ def main():
     ap.add_argument("--only-b4", action="store_true",
                     help="only the B=4 HBM-resident step (the profiled command)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="for counter runs: one eager B=4 step of the 52 layers, their 104 "
+                         "grouped-GEMM launches once more, then a 256 MiB device copy (the "
+                         "calibration kernel of known size); prints what was launched")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this path runs on one GPU; --gpus must be 1 (multi-GPU "
@@ -323,6 +446,23 @@ def main():
     ids4_static = torch.empty_like(ids4_dev[0])
     side = torch.cuda.Stream()
     ids4_static.copy_(ids4_dev[0])
+    if args.pmc_probe:
+        for l, L in enumerate(layers4):
+            L.apply(hb4[l + 1], hb4[l], tw4, ids4_static[l], gather=False)
+        gemm_launches(layers4)
+        a = torch.ones(256 << 20, dtype=torch.uint8, device=dev)
+        c = torch.empty_like(a)
+        torch.cuda.synchronize()
+        c.copy_(a)
+        torch.cuda.synchronize()
+        per, d = algorithmic_bytes(ids4[0], rows4)
+        print(json.dumps({"pmc_probe": "52 eager layer steps, then 104 grouped-GEMM launches, "
+                                       "then one 256 MiB device-to-device copy (last copy "
+                                       "kernel of the run)",
+                          "copy_bytes": 256 << 20, "gemm_launches": 2 * LAYERS,
+                          "algorithmic_bytes_per_launch": int(per),
+                          "distinct_experts_per_layer": round(float(d.mean()), 2)}), flush=True)
+        return
     gB = capture(torch, layers4, ids4_static, tw4, hb4, gather=False, side=side)
     log(f"setup {time.perf_counter() - t_setup:.1f}s; warmup {args.warmup} steps")
     run_steps(torch, gB, ids4_dev, ids4_static, 0, args.warmup)
@@ -372,6 +512,12 @@ def main():
         ms1, _ = time_steps(torch, g1, ids1_dev, ids1_static, args.warmup, args.steps)
         out["b1_ms_per_step"] = round(ms1, 4)
         log(f"B=1 HBM-resident step: {ms1:.3f} ms")
+        del g1, layers1
+        torch.cuda.synchronize()
+        out["lm_head_fp8"] = lm_head_fp8(torch, pkg, dev)
+        log(f"fp8 lm_head M=5: {out['lm_head_fp8']['us']} us")
+        out["lru_insert_sweep_us"] = lru_insert_sweep(torch, pkg, dev)
+        log(f"LRU insert sweep: {out['lru_insert_sweep_us']}")
         out["cpu_baseline"] = cpu_baseline(cpu_w13, cpu_w2, ids4, args.cpu_seconds)
     print(json.dumps(out), flush=True)
 

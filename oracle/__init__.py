@@ -10,10 +10,8 @@ Modules:
           and the warm start (kernels/lru/r4d_lru.hip, patches/.../r4d_mxfp4_moe.py.lru.diff)
   clru    ctypes binding of lru_oracle.c: an independent serial (argmin-per-insert) C
           restatement of the same functions, used to pin the numpy one
-  trace   seeded synthetic Zipf routing traces
   fp8     bit-exact float32 <-> OCP e4m3fn conversion and the block / group / SiLU quantizers
-  gemm    fp32-dequant grouped MoE GEMM, moe_sum, fp8 lm_head and W4 lm_head references
-  w4      the int4 group-128 quantizer / packer / dequantizer of this build's W4 format
+  gemm    fp32-dequant grouped MoE GEMM, moe_sum and the dense lm_head reference
 
 Parity status of every function is listed in each module's header.
 """

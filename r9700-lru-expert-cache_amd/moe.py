@@ -72,6 +72,11 @@ class LruMoELayer:
         self.M = max_tokens
         self.mtk = max_tokens * top_k
         self.npw1, self.npw2, self.sk1, self.sk2, self.wv = npw1, npw2, sk1, sk2, wv
+        for t in full.tensors():
+            slab = t[0].numel() * t.element_size()
+            if slab % 16:
+                raise ValueError(f"per-expert slab of {tuple(t.shape)} is {slab} B: the miss "
+                                 "gather copies 16-byte units (r4d_lru.hip:271-301)")
         hot = sorted(int(e) for e in hot_ids)
         if slots is None:
             idx = torch.tensor(hot, dtype=torch.int64)

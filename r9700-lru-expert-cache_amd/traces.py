@@ -1,4 +1,5 @@
-"""Seeded synthetic routing traces (test infrastructure only).
+"""Seeded synthetic routing traces: the workload generator of the benchmark, the smoke test and
+the tests (pure numpy; no kernel involved).
 
 zipf_trace(): the LRU-only workload -- E experts, `rows` routing rows per step, top-k drawn
 without replacement from p(rank r) ~ r^-s over a seeded random permutation of the experts,
@@ -70,3 +71,19 @@ def warm_hot(perm0: np.ndarray, S: int):
 def layer_trace(layer: int, steps: int, rows: int = 20, E: int = 512, k: int = 10,
                 s: float = 1.1, corr: float = 0.0, base: int = 1000):
     return zipf_trace(seed=base + layer, E=E, rows=rows, k=k, steps=steps, s=s, corr=corr)
+
+
+def insert_storm_ids(rng: np.random.Generator, hot: np.ndarray, E: int, mk: int,
+                     k: int) -> np.ndarray:
+    """Routing with exactly k distinct non-resident experts among mk ids (the rest drawn from
+    the resident set), shuffled: the insert-count sweep of tests/lru/bench_victim.py:43-79."""
+    hot = np.asarray(hot)
+    cold = np.setdiff1d(np.arange(E), hot)
+    k = min(k, len(cold))
+    nh = min(mk - k, len(hot))
+    routed = np.concatenate([rng.choice(cold, k, replace=False),
+                             rng.choice(hot, nh, replace=False)])
+    if len(routed) < mk:
+        routed = np.concatenate([routed, rng.choice(routed, mk - len(routed))])
+    rng.shuffle(routed)
+    return routed[:mk].astype(np.int32)

@@ -9,7 +9,8 @@ from __future__ import annotations
 import numpy as np
 
 from oracle import lru as olru
-from oracle import trace as otrace
+from conftest import load_pkg
+otrace = load_pkg().traces
 
 # (name, E, S, generator(rng, n) -> ids [rows, k], nsteps, max_distinct, max_inserts)
 def _skew(rng, n):

@@ -19,7 +19,8 @@ import pytest
 from conftest import gpu_case
 from oracle import fp8, gemm as ogemm
 from oracle import lru as olru
-from oracle import trace
+from conftest import load_pkg
+trace = load_pkg().traces
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu

@@ -201,12 +201,14 @@ def test_c1_trace_vs_reference_kernel(mine, ref):
             assert torch.equal(oa[i], ob[i]), f"step {n}: align output {i}"
 
 
-@pytest.mark.parametrize("rows", [1, 4, 20, 40, 205])
+@pytest.mark.parametrize("rows", [1, 4, 20, 40, 205, 4096])
 def test_fused_geometries(mine, rows):
-    """tests/lru/test_fused.py:265-280: mk = 10 .. 2050 incl. the chunked placement path."""
+    """tests/lru/test_fused.py:265-280: mk = 10 .. 2050 incl. the chunked placement path, and
+    a 4096-token prefill chunk (mk = 40960)."""
     E, S = 512, 257
     rng = np.random.default_rng(7)
-    from oracle import trace as otrace
+    from conftest import load_pkg
+    otrace = load_pkg().traces
     p = otrace.zipf_p(E, 1.1)
     _, s = victim_case(E=E, S=S, mk=10, k_cold=0, maxi=64, seed=3)
     s.max_distinct = max(1, int(S * 0.5))

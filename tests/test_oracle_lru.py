@@ -21,7 +21,8 @@ import pytest
 
 from lru_cases import POLICY_SUITES, VICTIM_CASES, c1_trace, policy_start, victim_case
 from oracle import clru, lru
-from oracle import trace as otrace
+from conftest import load_pkg
+otrace = load_pkg().traces
 
 BS = 16
 
