@@ -134,6 +134,16 @@ int rlu_gemm_fp8blk_m16(const void* qx, const float* xs, const void* w, const fl
  * rows % 16 == 0, K % 128 == 0, out must not overlap w. Returns -1 / -2 on bad sizes. */
 int rlu_shuffle_fp8_weight(const void* w, void* out, long long rows, int K, hipStream_t stream);
 
+/* Replaces the closed r4d_gemm_w4a16_nt_m64 behind draft_w4_lmhead_gemm / gemm_w4a16
+ * (kernels/draft_w4_lmhead.py:351-403), in this build's gfx950 W4 format:
+ *   y [M, N] bf16 = x [M, K] bf16 . (scale * (q - zero))^T, 1 <= M <= 16,
+ *   wq [N/16][K/128][64][16] bytes of int4 codes in bf16-MFMA B-operand order, sz
+ *   [N/16][K/128][16] u32 = bf16 scale | int16 zero << 16 (w4.pack_w4a16 writes both).
+ * wv: workgroups per CU of the persistent grid (0: 2). Returns -1 bad M / K / N / wv,
+ * -2 K % 128, N % 32 or K > 4096. */
+int rlu_gemm_w4_m16(const void* x, int M, int K, const void* wq, const unsigned* sz, void* y,
+                    int N, int wv, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

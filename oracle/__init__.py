@@ -12,6 +12,7 @@ Modules:
           restatement of the same functions, used to pin the numpy one
   fp8     bit-exact float32 <-> OCP e4m3fn conversion and the block / group / SiLU quantizers
   gemm    fp32-dequant grouped MoE GEMM, moe_sum and the dense lm_head reference
+  w4      the int4 group-128 quantizer, this build's W4 layout, and the float64 W4 GEMV
 
 Parity status of every function is listed in each module's header.
 """
