@@ -280,6 +280,45 @@ def lm_head_fp8(torch, pkg, dev, M=5, reps=20):
                 frac=round(gbs / HBM_PEAK_GBS, 4))
 
 
+def lm_head_w4(torch, pkg, dev, Ms=(1, 4, 8), reps=20):
+    """The W4 draft lm_head GEMV: vocab 151936 x 2560, int4 group-128 codes with bf16 scale and
+    integer zero (N(0, 0.02) weights, seed 5, packed with the clip search), x bf16 [M, 2560].
+    Two packed copies alternate (207 MB each, past the 256 MB last-level cache between
+    launches). Bytes per launch: codes + scale/zero words + activations + logits."""
+    N, K = 151936, 2560
+    w4 = pkg.w4
+    g = torch.Generator(device=dev).manual_seed(5)
+    P = []
+    for _ in range(2):
+        w = torch.randn(N, K, device=dev, generator=g) * 0.02
+        P.append(w4.pack_w4a16(w))
+        del w
+    torch.cuda.empty_cache()
+    out = {}
+    for M in Ms:
+        x = torch.randn(M, K, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16).to(dev)
+        y = torch.empty((M, P[0].n_pad), dtype=torch.bfloat16, device=dev)
+        nbytes = P[0].nbytes + M * K * 2 + M * N * 2
+        for i in range(2):
+            w4.gemm_w4a16(x, P[i], out=y)
+        torch.cuda.synchronize()
+        best = 1e30
+        for _ in range(3):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for i in range(reps):
+                w4.gemm_w4a16(x, P[i % 2], out=y)
+            b.record()
+            torch.cuda.synchronize()
+            best = min(best, a.elapsed_time(b) * 1e3 / reps)
+        gbs = nbytes / (best * 1e-6) / 1e9
+        out[f"M{M}"] = dict(us=round(best, 2), bytes=nbytes, achieved_gbs=round(gbs, 1),
+                            frac=round(gbs / HBM_PEAK_GBS, 4))
+    del P
+    torch.cuda.empty_cache()
+    return out
+
+
 def lru_insert_sweep(torch, pkg, dev, reps=50, rounds=5):
     """r4d_lru_fused time vs inserts per step at E=512, S=257 (the insert storm of
     tests/lru/bench_victim.py:43-79): routing with exactly k non-resident experts among mk ids,
@@ -517,6 +556,8 @@ def main():
         torch.cuda.synchronize()
         out["lm_head_fp8"] = lm_head_fp8(torch, pkg, dev)
         log(f"fp8 lm_head M=5: {out['lm_head_fp8']['us']} us")
+        out["lm_head_w4"] = lm_head_w4(torch, pkg, dev)
+        log(f"W4 lm_head: {out['lm_head_w4']}")
         out["lru_insert_sweep_us"] = lru_insert_sweep(torch, pkg, dev)
         log(f"LRU insert sweep: {out['lru_insert_sweep_us']}")
         out["cpu_baseline"] = cpu_baseline(cpu_w13, cpu_w2, ids4, args.cpu_seconds)

@@ -31,6 +31,8 @@ SIGNATURES: dict[str, tuple] = {
     "rlu_moe_gemm_split": (_I, [_P] * 14 + [_I] * 8 + [_P]),
     "rlu_shuffle_fp8_weight": (_I, [_P, _P, _LL, _I, _P]),
     "rlu_gemm_w4_m16": (_I, [_P, _I, _I, _P, _P, _P, _I, _I, _P]),
+    "rlu_moe_gemm_tiles": (_I, [_P, _P, _I, _P, _P, _P]),
+    "rlu_moe_gemm_fp8blk_tiled": (_I, [_P] * 8 + [_I, _P, _P] + [_I] * 5 + [_P]),
 }
 
 

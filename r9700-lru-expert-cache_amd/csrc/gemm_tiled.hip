@@ -1,0 +1,290 @@
+// The grouped fp8 GEMM in the MFMA regime (prefill: tens of rows per expert), same operands,
+// row contract and numerics as moe_gemm_k (gemm.hip), tiled for weight reuse:
+//
+//   tiles_k        from moe_align_block_size output (expert_ids per 16-row block, num_post_pad)
+//                  builds the tile list: each run of blocks of one expert is cut into tiles of
+//                  at most TMB blocks; a tile is (first block, block count). Blocks of expert -1
+//                  make no tile.
+//   tiled_k        one workgroup (4 waves) computes a TMB*16-row x 128-column tile: per 128-deep
+//                  K step it stages the tile's activation rows (gathered through sorted_ids) and
+//                  the 8 weight strips (fragment order, 2 KB contiguous each) in LDS, double-
+//                  buffered with one barrier per step, and each wave runs the 16 MFMAs of its
+//                  64 x 64 quadrant. The expert's weights stream from HBM once per tile instead
+//                  of once per 16-row block. Accumulation is acc += mfma * (xs * ws) per step,
+//                  as in moe_gemm_k, so both kernels give the same sums up to the association of
+//                  the (shared) per-step products -- each output is the same sequence of fma's.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "numerics.h"
+#include "rlu.h"
+#include "wave.h"
+
+namespace rlu {
+namespace tiled {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+
+constexpr int TMB = 8;           // 16-row blocks per tile
+constexpr int TBN = 128;         // columns per tile (8 strips of 16)
+constexpr int NTHR = 256;
+constexpr int MAXNB = 8192;      // blocks the tile builder handles (L = 131072 sorted ids)
+constexpr int TB_THR = 1024;
+
+__device__ __forceinline__ v8i pack8(v4u lo, v4u hi) {
+  v8i r;
+  r[0] = lo.x; r[1] = lo.y; r[2] = lo.z; r[3] = lo.w;
+  r[4] = hi.x; r[5] = hi.y; r[6] = hi.z; r[7] = hi.w;
+  return r;
+}
+
+__device__ __forceinline__ v4f mfma_f8(v8i a, v8i b) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, v4f{0.f, 0.f, 0.f, 0.f}, 0, 0,
+                                                          0, 127, 0, 127);
+}
+
+// ---- tile list ---------------------------------------------------------------------------
+__global__ __launch_bounds__(TB_THR) void tiles_k(const int* __restrict__ eids,
+                                                  const int* __restrict__ npad, int nb_max,
+                                                  int* __restrict__ tiles,
+                                                  int* __restrict__ ntiles) {
+  __shared__ int se[MAXNB];
+  __shared__ int part[TB_THR];
+  const int t = threadIdx.x;
+  int nb = npad[0] >> 4;
+  nb = nb < nb_max ? nb : nb_max;
+  for (int b = t; b < nb; b += TB_THR) se[b] = eids[b];
+  __syncthreads();
+  const int per = (nb + TB_THR - 1) / TB_THR;
+  const int lo = t * per;
+  const int hi = lo + per < nb ? lo + per : nb;
+  // run start of each block = the last block at or before it where the expert id changes
+  int last = -1;
+  for (int b = lo; b < hi; ++b)
+    if (b == 0 || se[b] != se[b - 1]) last = b;
+  part[t] = last;
+  __syncthreads();
+  for (int d = 1; d < TB_THR; d <<= 1) {            // inclusive max-scan over the segments
+    const int v = t >= d ? part[t - d] : -1;
+    __syncthreads();
+    if (v > part[t]) part[t] = v;
+    __syncthreads();
+  }
+  const int carry = t > 0 ? part[t - 1] : -1;     // run start entering this segment
+  __syncthreads();
+  int rs = carry;
+  int cnt = 0;
+  for (int b = lo; b < hi; ++b) {
+    if (b == 0 || se[b] != se[b - 1]) rs = b;
+    cnt += se[b] >= 0 && (b - rs) % TMB == 0;
+  }
+  part[t] = cnt;
+  __syncthreads();
+  for (int d = 1; d < TB_THR; d <<= 1) {            // inclusive sum-scan of the tile counts
+    const int v = t >= d ? part[t - d] : 0;
+    __syncthreads();
+    part[t] += v;
+    __syncthreads();
+  }
+  int pos = part[t] - cnt;
+  rs = carry;
+  for (int b = lo; b < hi; ++b) {
+    if (b == 0 || se[b] != se[b - 1]) rs = b;
+    if (se[b] >= 0 && (b - rs) % TMB == 0) {
+      int n = 1;
+      while (n < TMB && b + n < nb && se[b + n] == se[b]) ++n;
+      tiles[2 * pos] = b;
+      tiles[2 * pos + 1] = n;
+      ++pos;
+    }
+  }
+  if (t == TB_THR - 1) ntiles[0] = part[t];
+}
+
+// ---- the tiled GEMM ------------------------------------------------------------------------
+struct Smem {
+  v4u a[2][TMB * 128];           // [buf][block][half][lane]: 16 B per lane per half
+  v4u b[2][8 * 128];             // [buf][strip][half][lane]
+  float xs[2][TMB * 16];         // activation scale of each tile row at the staged step
+  int row[TMB * 16];             // sorted id of each tile row (>= mtk: padding)
+};
+
+template <bool TWT>
+__global__ __launch_bounds__(NTHR) void tiled_k(const uint8_t* __restrict__ qx,
+                                                const float* __restrict__ xs,
+                                                const uint8_t* __restrict__ wq,
+                                                const float* __restrict__ ws,
+                                                const int* __restrict__ sorted_ids,
+                                                const int* __restrict__ eids,
+                                                const int* __restrict__ tiles,
+                                                const int* __restrict__ ntiles_p,
+                                                uint16_t* __restrict__ y,
+                                                const float* __restrict__ tw, int mtk, int top_k,
+                                                int K, int N) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  Smem& S = *reinterpret_cast<Smem*>(smem_raw);
+  const int t = threadIdx.x;
+  const int lane = lane_id();
+  const int wv = uniform(t / WAVE);
+  const int rh = wv & 1, ch = wv >> 1;             // this wave's 64 x 64 quadrant
+  const int r16 = lane & 15, c4 = lane >> 4;
+  const int ncb = N / TBN;
+  const int nkg = K / 128;
+  const int nitems = ntiles_p[0] * ncb;
+
+  for (int item = blockIdx.x; item < nitems; item += gridDim.x) {
+    const int ti = item / ncb, cb = item - ti * ncb;
+    const int b0 = tiles[2 * ti], nbk = tiles[2 * ti + 1];
+    const int e = eids[b0];
+    const int n0 = cb * TBN;
+    __syncthreads();                                // previous item's epilogue reads of row[]
+    if (t < TMB * 16) {
+      const int blk = t >> 4;
+      S.row[t] = blk < nbk ? sorted_ids[(b0 + blk) * 16 + (t & 15)] : mtk;
+    }
+    __syncthreads();
+    const uint8_t* wbase = wq + ((size_t)e * N + n0) * K;
+    const float* wsr = ws + ((size_t)e * (N / 128) + cb) * nkg;
+
+    // staging: unit u (16 B) of A = (block u >> 7, half (u >> 6) & 1, lane u & 63); of B =
+    // (strip u >> 7, the strip's 2 KB in fragment order); 4 units of each per thread
+    v4u ra[4], rb[4];
+    float rx = 0.f;
+    auto load = [&](int kb) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int u = t + NTHR * q;
+        const int blk = u >> 7, l = u & 63, h = (u >> 6) & 1;
+        const int so = S.row[blk * 16 + (l & 15)];
+        ra[q] = v4u{0u, 0u, 0u, 0u};
+        if (so < mtk)
+          ra[q] = *reinterpret_cast<const v4u*>(qx + (size_t)(so / top_k) * K + kb * 128 +
+                                                64 * h + 16 * (l >> 4));
+        rb[q] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(
+            wbase + (size_t)(u >> 7) * 16 * K + (size_t)kb * 2048 + (u & 127) * 16));
+      }
+      if (t < TMB * 16) {
+        const int so = S.row[t];
+        rx = so < mtk ? xs[(size_t)(so / top_k) * nkg + kb] : 0.f;
+      }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        S.a[buf][t + NTHR * q] = ra[q];
+        S.b[buf][t + NTHR * q] = rb[q];
+      }
+      if (t < TMB * 16) S.xs[buf][t] = rx;
+    };
+
+    v4f acc[4][4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) acc[j][s] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int kb = 0; kb < nkg; ++kb) {
+      const int buf = kb & 1;
+      if (kb + 1 < nkg) load(kb + 1);
+      const float wsv = wsr[kb];
+      v8i bf[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        bf[s] = pack8(S.b[buf][(4 * ch + s) * 128 + lane], S.b[buf][(4 * ch + s) * 128 + 64 + lane]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int blk = 4 * rh + j;
+        if (blk < nbk) {
+          const v8i af = pack8(S.a[buf][blk * 128 + lane], S.a[buf][blk * 128 + 64 + lane]);
+          const v4f xr = *reinterpret_cast<const v4f*>(&S.xs[buf][blk * 16 + 4 * c4]);
+          v4f f;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) f[i] = xr[i] * wsv;
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            const v4f d = mfma_f8(af, bf[s]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[j][s][i] = fmaf(d[i], f[i], acc[j][s][i]);
+          }
+        }
+      }
+      if (kb + 1 < nkg) store(buf ^ 1);
+      __syncthreads();
+    }
+    // epilogue: rows this lane holds, routed weight, bf16, live rows only
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int blk = 4 * rh + j;
+      if (blk < nbk) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int so = S.row[blk * 16 + 4 * c4 + i];
+          if (so < mtk) {
+            const float wgt = TWT ? tw[so] : 1.0f;
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+              y[(size_t)so * N + n0 + (4 * ch + s) * 16 + r16] = f32_to_bf16(acc[j][s][i] * wgt);
+          }
+        }
+      }
+    }
+  }
+}
+
+static int num_cus() {
+  static int n = 0;
+  if (!n) {
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+  }
+  return n;
+}
+
+}  // namespace tiled
+}  // namespace rlu
+
+extern "C" {
+
+int rlu_moe_gemm_tiles(const int* expert_ids, const int* num_post_pad, int nb_max, int* tiles,
+                       int* ntiles, hipStream_t stream) {
+  using namespace rlu::tiled;
+  if (nb_max <= 0 || nb_max > MAXNB || !expert_ids || !num_post_pad || !tiles || !ntiles)
+    return -1;
+  hipLaunchKernelGGL(tiles_k, dim3(1), dim3(TB_THR), 0, stream, expert_ids, num_post_pad, nb_max,
+                     tiles, ntiles);
+  return (int)hipGetLastError();
+}
+
+int rlu_moe_gemm_fp8blk_tiled(const void* qx, const float* xs, const void* wq, const float* ws,
+                              const int* sorted_ids, const int* expert_ids, const int* tiles,
+                              const int* ntiles, int max_tiles, const float* topk_weights,
+                              void* y, int mtk, int top_k, int K, int N, int wv,
+                              hipStream_t stream) {
+  using namespace rlu::tiled;
+  if (mtk < 0 || top_k < 1 || K <= 0 || N <= 0 || max_tiles <= 0) return -1;
+  if (K % 128 || N % TBN) return -2;
+  if (wv < 0 || wv > 16) return -5;
+  if (mtk == 0) return 0;
+  const int items = max_tiles * (N / TBN);
+  int grid = num_cus() * (wv ? wv : 2);
+  if (grid > items) grid = items;
+  const size_t lds = sizeof(Smem);
+  if (topk_weights)
+    hipLaunchKernelGGL(tiled_k<true>, dim3(grid), dim3(NTHR), lds, stream, (const uint8_t*)qx,
+                       xs, (const uint8_t*)wq, ws, sorted_ids, expert_ids, tiles, ntiles,
+                       (uint16_t*)y, topk_weights, mtk, top_k, K, N);
+  else
+    hipLaunchKernelGGL(tiled_k<false>, dim3(grid), dim3(NTHR), lds, stream, (const uint8_t*)qx,
+                       xs, (const uint8_t*)wq, ws, sorted_ids, expert_ids, tiles, ntiles,
+                       (uint16_t*)y, nullptr, mtk, top_k, K, N);
+  return (int)hipGetLastError();
+}
+
+}  // extern "C"

@@ -12,6 +12,8 @@ Mirrors the reference's Python entry points for these stages:
   shuffle_fp8_weight              shuffle_weight_gfx1201 (kernels/fp8_target_lmhead.py:47,64),
                                   here the gfx950 MFMA fragment order every GEMM reads
   pack_fp8_block                  kernels/fp8_target_lmhead.py:44-66
+  moe_gemm_tiled                  the grouped GEMM for prefill-sized inputs (no counterpart:
+                                  the reference ran one closed kernel at every M)
 Errors from the C-ABI raise RuntimeError; there is no fallback implementation.
 """
 from __future__ import annotations
@@ -158,3 +160,35 @@ def pack_fp8_block(w: torch.Tensor, rows: int = 4096) -> tuple[torch.Tensor, tor
         q[r0:r1] = (wf / scale).clamp(-448.0, 448.0).to(FP8).view(r1 - r0, K)
         ws[r0 // 128:r1 // 128] = scale.view((r1 - r0) // 128, K // 128)
     return shuffle_fp8_weight(q), ws
+
+
+def moe_gemm_tiles(expert_ids: torch.Tensor, num_post_pad: torch.Tensor,
+                   out: torch.Tensor | None = None) -> torch.Tensor:
+    """The tile list of an align output: int32 [2 * nb + 1] = (first block, block count) per
+    tile, then the tile count at the end."""
+    nb = expert_ids.numel()
+    ws = torch.empty(2 * nb + 1, dtype=torch.int32, device=expert_ids.device) if out is None else out
+    rc = lib().rlu_moe_gemm_tiles(_p(expert_ids), _p(num_post_pad), nb, _p(ws),
+                                  _P(ws.data_ptr() + 8 * nb), _P(stream_ptr()))
+    check(rc, "rlu_moe_gemm_tiles")
+    return ws
+
+
+def moe_gemm_tiled(y: torch.Tensor, qx: torch.Tensor, x_scale: torch.Tensor, wq: torch.Tensor,
+                   ws_t: torch.Tensor, sorted_ids: torch.Tensor, expert_ids: torch.Tensor,
+                   num_post_pad: torch.Tensor, topk_weights: torch.Tensor | None, mtk: int,
+                   top_k: int, tiles: torch.Tensor | None = None, wv: int = 0) -> None:
+    """_r4d_fp8_moe_gemm_into for prefill-sized inputs: same operands and row contract, one
+    workgroup per 128-row x 128-column tile of one expert (bit-identical to the decode kernel
+    with sk = 1). `tiles` is an int32 workspace of 2 * expert_ids.numel() + 1 entries."""
+    K = qx.shape[1]
+    N = wq.shape[1]
+    nb = expert_ids.numel()
+    assert y.shape == (mtk, N) and y.dtype == torch.bfloat16 and y.is_contiguous()
+    assert qx.dtype == FP8 and wq.dtype == FP8 and wq.shape[2] == K
+    tiles = moe_gemm_tiles(expert_ids, num_post_pad, tiles)
+    rc = lib().rlu_moe_gemm_fp8blk_tiled(
+        _p(qx), _p(x_scale), _p(wq), _p(ws_t), _p(sorted_ids), _p(expert_ids), _p(tiles),
+        _P(tiles.data_ptr() + 8 * nb), nb, _p(topk_weights), _p(y), mtk, top_k, K, N, wv,
+        _P(stream_ptr()))
+    check(rc, "rlu_moe_gemm_fp8blk_tiled")

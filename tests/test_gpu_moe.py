@@ -461,3 +461,125 @@ def test_moe_gemm_split_one_launch_equals_two_calls(pkg, ops, layer):
     torch.cuda.synchronize()
     assert not torch.isnan(y1).any()
     assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+
+
+# ---- the tiled (prefill) grouped GEMM ---------------------------------------------------------
+def tiles_ref(eids, npad, tmb=8):
+    """The tile list by walking the align output: each run of one expert's blocks cut into
+    tiles of at most tmb blocks; expert -1 blocks make none."""
+    nb = int(npad) // 16
+    out = []
+    b = 0
+    while b < nb:
+        e = eids[b]
+        r = b
+        while r < nb and eids[r] == e:
+            r += 1
+        if e >= 0:
+            for s in range(b, r, tmb):
+                out.append((s, min(tmb, r - s)))
+        b = r
+    return out
+
+
+@pytest.mark.parametrize("M,E_used", [(256, 40), (600, 40), (37, 12)])
+def test_moe_gemm_tile_list(ops, M, E_used):
+    ids = routing(M, 10, E_used, seed=M)
+    s, e, n = align_all(ids, E_used)
+    e2 = e.copy()
+    if len(e2) > 3:
+        e2[2] = -1                                   # a skipped block
+    tl = ops.moe_gemm_tiles(*to_dev_i32(e2, n)[0:2])
+    torch.cuda.synchronize()
+    got = tl.cpu().numpy()
+    nt = int(got[-1])
+    want = tiles_ref(e2, n[0])
+    assert nt == len(want)
+    assert [tuple(x) for x in got[:2 * nt].reshape(-1, 2)] == want
+
+
+@pytest.mark.parametrize("M", [256, 600])
+def test_moe_gemm_tiled_equals_decode_kernel(ops, layer, M):
+    """Prefill-sized routing (64 / 150 rows per expert): the tiled kernel and the decode kernel
+    with sk = 1 run the same per-step fma sequence, so their outputs are bit-identical."""
+    E, H, I = layer["E"], layer["H"], layer["I"]
+    top_k = 10
+    ids = routing(M, top_k, E, seed=M + 1)
+    mtk = ids.size
+    al = to_dev_i32(*align_all(ids, E))
+    rng = np.random.default_rng(M)
+    x = fp8.bf16_round(rng.standard_normal((M, H)).astype(np.float32))
+    qx, xs = fp8.group_quant(x, 128)
+    qx_t = torch.from_numpy(qx).to(DEV).view(torch.float8_e4m3fn)
+    xs_t = torch.from_numpy(xs).to(DEV)
+    yt = torch.full((mtk, 2 * I), float("nan"), dtype=torch.bfloat16, device=DEV)
+    yd = torch.full_like(yt, float("nan"))
+    gpu_case(f"tiled gemm1 M={M}")
+    ops.moe_gemm_tiled(yt, qx_t, xs_t, layer["w13t"], layer["w13s"], *al, None, mtk, top_k)
+    run_gemm(ops, yd, qx_t, xs_t, layer["w13t"], layer["w13s"], al, None, mtk, top_k, npw=2, sk=1)
+    torch.cuda.synchronize()
+    assert not torch.isnan(yt).any()
+    assert torch.equal(yt.view(torch.int16), yd.view(torch.int16))
+    # down projection with routed weights
+    a = fp8.bf16_round(rng.standard_normal((mtk, I)).astype(np.float32))
+    q2, s2 = fp8.group_quant(a, 128)
+    q2_t = torch.from_numpy(q2).to(DEV).view(torch.float8_e4m3fn)
+    s2_t = torch.from_numpy(s2).to(DEV)
+    tw = torch.from_numpy(rng.random(mtk).astype(np.float32)).to(DEV)
+    zt = torch.full((mtk, H), float("nan"), dtype=torch.bfloat16, device=DEV)
+    zd = torch.full_like(zt, float("nan"))
+    gpu_case(f"tiled gemm2 M={M}")
+    ops.moe_gemm_tiled(zt, q2_t, s2_t, layer["w2t"], layer["w2s"], *al, tw, mtk, 1)
+    run_gemm(ops, zd, q2_t, s2_t, layer["w2t"], layer["w2s"], al, tw, mtk, 1, npw=2, sk=1)
+    torch.cuda.synchronize()
+    assert not torch.isnan(zt).any()
+    assert torch.equal(zt.view(torch.int16), zd.view(torch.int16))
+    if M == 256:
+        used = sorted(set(ids.reshape(-1).tolist()))
+        wq, ws = ref_from(layer["w13q"], layer["w13s"], used)
+        want = ogemm.moe_gemm(qx, xs, _Lazy(wq), _Lazy(ws), *align_all(ids, E), mtk, top_k)
+        assert ogemm.rel_err(np_from_bf16(yt), want) <= TOL
+
+
+def test_moe_gemm_tiled_row_contract_and_graph(ops, layer):
+    """A block of expert -1 is skipped (its rows stay NaN); graph replay equals eager."""
+    E, H, I = layer["E"], layer["H"], layer["I"]
+    M, top_k = 128, 10
+    ids = routing(M, top_k, E, seed=5)
+    mtk = ids.size
+    s, e, n = align_all(ids, E)
+    e2 = e.copy()
+    e2[1] = -1
+    al = to_dev_i32(s, e2, n)
+    x = fp8.bf16_round(np.random.default_rng(6).standard_normal((M, H)).astype(np.float32))
+    qx, xs = fp8.group_quant(x, 128)
+    qx_t = torch.from_numpy(qx).to(DEV).view(torch.float8_e4m3fn)
+    xs_t = torch.from_numpy(xs).to(DEV)
+    y = torch.full((mtk, 2 * I), float("nan"), dtype=torch.bfloat16, device=DEV)
+    tiles = torch.empty(2 * e2.size + 1, dtype=torch.int32, device=DEV)
+    gpu_case("tiled gemm row contract")
+    ops.moe_gemm_tiled(y, qx_t, xs_t, layer["w13t"], layer["w13s"], *al, None, mtk, top_k,
+                       tiles=tiles)
+    torch.cuda.synchronize()
+    skipped = s[16:32][s[16:32] < mtk]
+    written = ~torch.isnan(y).any(dim=1).cpu().numpy()
+    live = np.zeros(mtk, bool)
+    live[s[:n[0]][s[:n[0]] < mtk]] = True
+    live[skipped] = False
+    assert np.array_equal(written, live)
+    g = torch.cuda.CUDAGraph()
+    y2 = torch.full_like(y, float("nan"))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        ops.moe_gemm_tiled(y2, qx_t, xs_t, layer["w13t"], layer["w13s"], *al, None, mtk, top_k,
+                           tiles=tiles)
+    torch.cuda.current_stream().wait_stream(side)
+    with torch.cuda.graph(g):
+        ops.moe_gemm_tiled(y2, qx_t, xs_t, layer["w13t"], layer["w13s"], *al, None, mtk, top_k,
+                           tiles=tiles)
+    for _ in range(3):
+        y2.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y2.view(torch.int16), y.view(torch.int16))
