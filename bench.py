@@ -319,6 +319,63 @@ def lm_head_w4(torch, pkg, dev, Ms=(1, 4, 8), reps=20):
     return out
 
 
+def prefill_gemm(torch, pkg, dev, T=4096, reps=3):
+    """The grouped GEMMs in the MFMA regime: a 4096-token prefill chunk, top-10 uniform over
+    the 512 experts (seed 0), all experts HBM-resident (w13 / w2 fp8, fragment order), through
+    the fused LRU + align (read-through: 512 distinct > 128) and the tiled kernel. Reports each
+    GEMM's time, its dense TFLOP/s (2 mk N K) and its weight bytes / time."""
+    ops = pkg.ops
+    g = torch.Generator(device=dev).manual_seed(7)
+    w13 = torch.randint(-100, 100, (E, 2 * I, H), device=dev, generator=g,
+                        dtype=torch.int8).view(torch.float8_e4m3fn)
+    w2 = torch.randint(-100, 100, (E, H, I), device=dev, generator=g,
+                       dtype=torch.int8).view(torch.float8_e4m3fn)
+    w13s = torch.rand(E, 2 * I // 128, H // 128, device=dev, generator=g) * 1e-3
+    w2s = torch.rand(E, H // 128, I // 128, device=dev, generator=g) * 1e-3
+    rng = np.random.default_rng(0)
+    ids = np.stack([rng.choice(E, TOPK, replace=False) for _ in range(T)]).astype(np.int32)
+    cache = pkg.LruCache.build(E, range(E), None, dev)
+    al = cache.alloc_align(ids.size)
+    (sh, eh, nh), _ = cache.fused(torch.from_numpy(ids).to(dev), out=al)
+    mtk = ids.size
+    x = torch.randint(-100, 100, (T, H), device=dev, generator=g,
+                      dtype=torch.int8).view(torch.float8_e4m3fn)
+    xs = torch.rand(T, H // 128, device=dev, generator=g)
+    x2 = torch.randint(-100, 100, (mtk, I), device=dev, generator=g,
+                       dtype=torch.int8).view(torch.float8_e4m3fn)
+    s2 = torch.rand(mtk, I // 128, device=dev, generator=g)
+    tw = torch.rand(mtk, device=dev, generator=g)
+    y1 = torch.empty(mtk, 2 * I, dtype=torch.bfloat16, device=dev)
+    y2 = torch.empty(mtk, H, dtype=torch.bfloat16, device=dev)
+    tiles = torch.empty(2 * eh.numel() + 1, dtype=torch.int32, device=dev)
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        best = 1e30
+        for _ in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            torch.cuda.synchronize()
+            best = min(best, a.elapsed_time(b) * 1e3)
+        return best
+    u1 = timed(lambda: ops.moe_gemm_tiled(y1, x, xs, w13, w13s, sh, eh, nh, None, mtk, TOPK,
+                                          tiles=tiles, wv=2))
+    u2 = timed(lambda: ops.moe_gemm_tiled(y2, x2, s2, w2, w2s, sh, eh, nh, tw, mtk, 1,
+                                          tiles=tiles, wv=2))
+    res = {}
+    for name, us, n, k in (("gate_up", u1, 2 * I, H), ("down", u2, H, I)):
+        res[name] = dict(us=round(us, 1), tflops=round(2.0 * mtk * n * k / us / 1e6, 1),
+                         weight_gbs=round(E * n * k / us / 1e3, 1))
+    res["tokens"], res["rows_per_expert"] = T, round(mtk / E, 1)
+    res["tiles"] = int(tiles[-1].item())
+    del w13, w2
+    torch.cuda.empty_cache()
+    return res
+
+
 def lru_insert_sweep(torch, pkg, dev, reps=50, rounds=5):
     """r4d_lru_fused time vs inserts per step at E=512, S=257 (the insert storm of
     tests/lru/bench_victim.py:43-79): routing with exactly k non-resident experts among mk ids,
@@ -558,6 +615,8 @@ def main():
         log(f"fp8 lm_head M=5: {out['lm_head_fp8']['us']} us")
         out["lm_head_w4"] = lm_head_w4(torch, pkg, dev)
         log(f"W4 lm_head: {out['lm_head_w4']}")
+        out["prefill_4096"] = prefill_gemm(torch, pkg, dev)
+        log(f"prefill 4096 tokens: {out['prefill_4096']}")
         out["lru_insert_sweep_us"] = lru_insert_sweep(torch, pkg, dev)
         log(f"LRU insert sweep: {out['lru_insert_sweep_us']}")
         out["cpu_baseline"] = cpu_baseline(cpu_w13, cpu_w2, ids4, args.cpu_seconds)

@@ -144,8 +144,8 @@ int rlu_moe_gemm_tiles(const int* expert_ids, const int* num_post_pad, int nb_ma
 
 /* Step 2: the same product, row contract and per-step accumulation as
  * r4d_gemm_moe_fp8blk_nt_b16 with sk = 1 (equal to it bit for bit), one workgroup per 128-row x
- * 128-column tile so an expert's weights are read once per tile. max_tiles bounds the device
- * count (the align output's block count). N % 128 == 0. Returns -1 / -2 / -5 as above. */
+ * 256-column tile so an expert's weights are read once per tile. max_tiles bounds the device
+ * count (the align output's block count). N % 256 == 0. Returns -1 / -2 / -5 as above. */
 int rlu_moe_gemm_fp8blk_tiled(const void* qx, const float* xs, const void* wq, const float* ws,
                               const int* sorted_ids, const int* expert_ids, const int* tiles,
                               const int* ntiles, int max_tiles, const float* topk_weights,

@@ -5,11 +5,12 @@
 //                  builds the tile list: each run of blocks of one expert is cut into tiles of
 //                  at most TMB blocks; a tile is (first block, block count). Blocks of expert -1
 //                  make no tile.
-//   tiled_k        one workgroup (4 waves) computes a TMB*16-row x 128-column tile: per 128-deep
+//   tiled_k        one workgroup (8 waves) computes a TMB*16-row x 256-column tile: per 128-deep
 //                  K step it stages the tile's activation rows (gathered through sorted_ids) and
-//                  the 8 weight strips (fragment order, 2 KB contiguous each) in LDS, double-
-//                  buffered with one barrier per step, and each wave runs the 16 MFMAs of its
-//                  64 x 64 quadrant. The expert's weights stream from HBM once per tile instead
+//                  the 16 weight strips (fragment order, 2 KB contiguous each) in LDS, double-
+//                  buffered with one barrier per step; wave w runs the MFMAs of blocks
+//                  w % 2, w % 2 + 2, ... (interleaved, so a short tile still splits evenly) and
+//                  strips 4 (w / 2) .. 4 (w / 2) + 3. The expert's weights stream from HBM once per tile instead
 //                  of once per 16-row block. Accumulation is acc += mfma * (xs * ws) per step,
 //                  as in moe_gemm_k, so both kernels give the same sums up to the association of
 //                  the (shared) per-step products -- each output is the same sequence of fma's.
@@ -28,8 +29,9 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 
 constexpr int TMB = 8;           // 16-row blocks per tile
-constexpr int TBN = 128;         // columns per tile (8 strips of 16)
-constexpr int NTHR = 256;
+constexpr int TBN = 256;         // columns per tile (16 strips of 16)
+constexpr int NSTRIP = TBN / 16;
+constexpr int NTHR = 512;        // 8 waves: 2 interleaved block sets x 4 column quarters
 constexpr int MAXNB = 8192;      // blocks the tile builder handles (L = 131072 sorted ids)
 constexpr int TB_THR = 1024;
 
@@ -106,7 +108,7 @@ __global__ __launch_bounds__(TB_THR) void tiles_k(const int* __restrict__ eids,
 // ---- the tiled GEMM ------------------------------------------------------------------------
 struct Smem {
   v4u a[2][TMB * 128];           // [buf][block][half][lane]: 16 B per lane per half
-  v4u b[2][8 * 128];             // [buf][strip][half][lane]
+  v4u b[2][NSTRIP * 128];        // [buf][strip][half][lane]
   float xs[2][TMB * 16];         // activation scale of each tile row at the staged step
   int row[TMB * 16];             // sorted id of each tile row (>= mtk: padding)
 };
@@ -128,7 +130,7 @@ __global__ __launch_bounds__(NTHR) void tiled_k(const uint8_t* __restrict__ qx,
   const int t = threadIdx.x;
   const int lane = lane_id();
   const int wv = uniform(t / WAVE);
-  const int rh = wv & 1, ch = wv >> 1;             // this wave's 64 x 64 quadrant
+  const int rh = wv & 1, ch = wv >> 1;             // blocks rh, rh + 2, ...; strips 4 ch ..
   const int r16 = lane & 15, c4 = lane >> 4;
   const int ncb = N / TBN;
   const int nkg = K / 128;
@@ -146,15 +148,17 @@ __global__ __launch_bounds__(NTHR) void tiled_k(const uint8_t* __restrict__ qx,
     }
     __syncthreads();
     const uint8_t* wbase = wq + ((size_t)e * N + n0) * K;
-    const float* wsr = ws + ((size_t)e * (N / 128) + cb) * nkg;
+    // this wave's strips 4 ch .. 4 ch + 3 lie in the 128-column scale block n0 / 128 + ch / 2
+    const float* wsr = ws + ((size_t)e * (N / 128) + n0 / 128 + (ch >> 1)) * nkg;
 
-    // staging: unit u (16 B) of A = (block u >> 7, half (u >> 6) & 1, lane u & 63); of B =
-    // (strip u >> 7, the strip's 2 KB in fragment order); 4 units of each per thread
-    v4u ra[4], rb[4];
+    // staging: unit u (16 B) of A = (block u >> 7, half (u >> 6) & 1, lane u & 63), 2 per
+    // thread; of B = (strip u >> 7, the strip's 2 KB in fragment order), 4 per thread
+    constexpr int QA = TMB * 128 / NTHR, QB = NSTRIP * 128 / NTHR;
+    v4u ra[QA], rb[QB];
     float rx = 0.f;
     auto load = [&](int kb) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
+      for (int q = 0; q < QA; ++q) {
         const int u = t + NTHR * q;
         const int blk = u >> 7, l = u & 63, h = (u >> 6) & 1;
         const int so = S.row[blk * 16 + (l & 15)];
@@ -162,6 +166,10 @@ __global__ __launch_bounds__(NTHR) void tiled_k(const uint8_t* __restrict__ qx,
         if (so < mtk)
           ra[q] = *reinterpret_cast<const v4u*>(qx + (size_t)(so / top_k) * K + kb * 128 +
                                                 64 * h + 16 * (l >> 4));
+      }
+#pragma unroll
+      for (int q = 0; q < QB; ++q) {
+        const int u = t + NTHR * q;
         rb[q] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(
             wbase + (size_t)(u >> 7) * 16 * K + (size_t)kb * 2048 + (u & 127) * 16));
       }
@@ -172,10 +180,9 @@ __global__ __launch_bounds__(NTHR) void tiled_k(const uint8_t* __restrict__ qx,
     };
     auto store = [&](int buf) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        S.a[buf][t + NTHR * q] = ra[q];
-        S.b[buf][t + NTHR * q] = rb[q];
-      }
+      for (int q = 0; q < QA; ++q) S.a[buf][t + NTHR * q] = ra[q];
+#pragma unroll
+      for (int q = 0; q < QB; ++q) S.b[buf][t + NTHR * q] = rb[q];
       if (t < TMB * 16) S.xs[buf][t] = rx;
     };
 
@@ -198,7 +205,7 @@ __global__ __launch_bounds__(NTHR) void tiled_k(const uint8_t* __restrict__ qx,
         bf[s] = pack8(S.b[buf][(4 * ch + s) * 128 + lane], S.b[buf][(4 * ch + s) * 128 + 64 + lane]);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int blk = 4 * rh + j;
+        const int blk = rh + 2 * j;
         if (blk < nbk) {
           const v8i af = pack8(S.a[buf][blk * 128 + lane], S.a[buf][blk * 128 + 64 + lane]);
           const v4f xr = *reinterpret_cast<const v4f*>(&S.xs[buf][blk * 16 + 4 * c4]);
@@ -219,7 +226,7 @@ __global__ __launch_bounds__(NTHR) void tiled_k(const uint8_t* __restrict__ qx,
     // epilogue: rows this lane holds, routed weight, bf16, live rows only
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int blk = 4 * rh + j;
+      const int blk = rh + 2 * j;
       if (blk < nbk) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {

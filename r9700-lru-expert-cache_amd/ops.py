@@ -179,8 +179,9 @@ def moe_gemm_tiled(y: torch.Tensor, qx: torch.Tensor, x_scale: torch.Tensor, wq:
                    num_post_pad: torch.Tensor, topk_weights: torch.Tensor | None, mtk: int,
                    top_k: int, tiles: torch.Tensor | None = None, wv: int = 0) -> None:
     """_r4d_fp8_moe_gemm_into for prefill-sized inputs: same operands and row contract, one
-    workgroup per 128-row x 128-column tile of one expert (bit-identical to the decode kernel
-    with sk = 1). `tiles` is an int32 workspace of 2 * expert_ids.numel() + 1 entries."""
+    workgroup per 128-row x 256-column tile of one expert (bit-identical to the decode kernel
+    with sk = 1); N % 256 == 0. `tiles` is an int32 workspace of 2 * expert_ids.numel() + 1
+    entries."""
     K = qx.shape[1]
     N = wq.shape[1]
     nb = expert_ids.numel()
