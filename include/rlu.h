@@ -51,6 +51,20 @@ int r4d_lru_fused(const int* topk_ids, int mk, int E, int S, int max_distinct,
                   int* npad_hot, int* sorted_cold, int* eids_cold, int* npad_cold,
                   hipStream_t stream);
 
+/* No counterpart in the reference: r4d_lru_fused plus, in the same launch (workgroups 1..rows,
+ * one row each, beside the cache's workgroup 0), the per-token-group-128 e4m3 quant of the
+ * layer's hidden state x [rows, K] bf16 (ldx elements apart) into q [rows, K] and scale
+ * [rows, K / 128] -- the quant the reference launched separately before its first GEMM
+ * (patches/.../r4dhip.py.diff:22-34), bit for bit rlu_quant_fp8_group with group 128.
+ * Returns r4d_lru_fused's codes, -1 for bad rows / K / ldx / null buffers, -2 K % 128. */
+int rlu_lru_fused_quant(const int* topk_ids, int mk, int E, int S, int max_distinct,
+                        int max_inserts, int* table, int* map_cold, int* slot_expert,
+                        long long* slot_stamp, unsigned char* routed, long long* step, int* miss,
+                        int* n_miss, int bs, int L, int NB, int* sorted_hot, int* eids_hot,
+                        int* npad_hot, int* sorted_cold, int* eids_cold, int* npad_cold,
+                        const void* x, int rows, int K, int ldx, void* q, float* scale,
+                        hipStream_t stream);
+
 int r4d_lru_gather(void* d0, const void* s0, long b0, void* d1, const void* s1, long b1,
                    void* d2, const void* s2, long b2, void* d3, const void* s3, long b3,
                    void* d4, const void* s4, long b4, void* d5, const void* s5, long b5,

@@ -30,6 +30,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "quant_row.h"
 #include "rlu.h"
 #include "wave.h"
 
@@ -363,6 +364,16 @@ __device__ __forceinline__ void place_buckets(LruLds& L, int* __restrict__ oh,
   }
 }
 
+// The per-token-group-128 quant of the layer's hidden state, run by workgroups 1.. of the fused
+// launch (one row each) while workgroup 0 runs the cache: the two are independent and both
+// feed the first GEMM, so one launch serves both.
+struct QuantJob {
+  const uint16_t* x;
+  int K, ldx;
+  uint8_t* q;
+  float* scale;
+};
+
 template <bool ALIGN>
 __global__ __launch_bounds__(NT) void lru_k(
     const int* __restrict__ ids, int mk, int E, int S, int max_distinct, int max_inserts,
@@ -371,7 +382,13 @@ __global__ __launch_bounds__(NT) void lru_k(
     long long* __restrict__ step, int* __restrict__ miss, int* __restrict__ n_miss, int bs,
     int Lsz, int NB, int* __restrict__ sorted_hot, int* __restrict__ eids_hot,
     int* __restrict__ npad_hot, int* __restrict__ sorted_cold, int* __restrict__ eids_cold,
-    int* __restrict__ npad_cold) {
+    int* __restrict__ npad_cold, QuantJob qj) {
+  if (blockIdx.x > 0) {
+    const int r = blockIdx.x - 1;
+    group_quant_row128(qj.x + (size_t)r * qj.ldx, qj.K, qj.q + (size_t)r * qj.K,
+                       qj.scale + (size_t)r * (qj.K / 128));
+    return;
+  }
   __shared__ LruLds L;
   const int t = threadIdx.x;
   const int w = t / WAVE;
@@ -705,7 +722,7 @@ int r4d_lru_manage(const int* topk_ids, int mk, int E, int S, int max_distinct,
   hipLaunchKernelGGL(rlu::lru_k<false>, dim3(1), dim3(rlu::NT), 0, stream, topk_ids, mk, E, S,
                      max_distinct, max_inserts, table, map_cold, slot_expert, slot_stamp,
                      routed, step, miss, n_miss, 1, 0, 0, nullptr, nullptr, nullptr, nullptr,
-                     nullptr, nullptr);
+                     nullptr, nullptr, rlu::QuantJob{});
   return (int)hipGetLastError();
 }
 
@@ -722,7 +739,30 @@ int r4d_lru_fused(const int* topk_ids, int mk, int E, int S, int max_distinct,
   hipLaunchKernelGGL(rlu::lru_k<true>, dim3(1), dim3(rlu::NT), 0, stream, topk_ids, mk, E, S,
                      max_distinct, max_inserts, table, map_cold, slot_expert, slot_stamp,
                      routed, step, miss, n_miss, bs, L, NB, sorted_hot, eids_hot, npad_hot,
-                     sorted_cold, eids_cold, npad_cold);
+                     sorted_cold, eids_cold, npad_cold, rlu::QuantJob{});
+  return (int)hipGetLastError();
+}
+
+// r4d_lru_fused plus, in the same launch, the per-token-group-128 e4m3 quant of x [rows, K]
+// bf16 (ldx elements apart) into q [rows, K] and scale [rows, K / 128], exactly as
+// rlu_quant_fp8_group with group 128.
+int rlu_lru_fused_quant(const int* topk_ids, int mk, int E, int S, int max_distinct,
+                        int max_inserts, int* table, int* map_cold, int* slot_expert,
+                        long long* slot_stamp, unsigned char* routed, long long* step, int* miss,
+                        int* n_miss, int bs, int L, int NB, int* sorted_hot, int* eids_hot,
+                        int* npad_hot, int* sorted_cold, int* eids_cold, int* npad_cold,
+                        const void* x, int rows, int K, int ldx, void* q, float* scale,
+                        hipStream_t stream) {
+  if (E <= 0 || E > rlu::MAXE || S <= 0 || S > rlu::MAXS) return -1;
+  if (bs <= 0 || L <= 0 || NB <= 0 || mk < 0) return -1;
+  if (max_inserts < 0 || max_inserts > rlu::MAXINS) return -1;
+  if (rows < 0 || K <= 0 || ldx < K || (rows > 0 && (!x || !q || !scale))) return -1;
+  if (K % 128 || ldx % 8) return -2;
+  hipLaunchKernelGGL(rlu::lru_k<true>, dim3(1 + rows), dim3(rlu::NT), 0, stream, topk_ids, mk,
+                     E, S, max_distinct, max_inserts, table, map_cold, slot_expert, slot_stamp,
+                     routed, step, miss, n_miss, bs, L, NB, sorted_hot, eids_hot, npad_hot,
+                     sorted_cold, eids_cold, npad_cold,
+                     rlu::QuantJob{(const uint16_t*)x, K, ldx, (uint8_t*)q, scale});
   return (int)hipGetLastError();
 }
 

@@ -11,28 +11,19 @@
 //                     patches/.../r4d_mxfp4_moe.py.lru.diff:696), float32 accumulation in k order.
 //
 // Layout: one workgroup per row; each lane owns 8 consecutive columns, so a 16-lane DPP row
-// covers exactly one 128-column group and the group amax is a 4-step DPP reduction.
+// covers exactly one 128-column group and the group amax is a 4-step DPP reduction
+// (quant_row.h).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #include "numerics.h"
+#include "quant_row.h"
 #include "rlu.h"
 #include "wave.h"
 
 namespace rlu {
 
 constexpr int QT = 256;   // threads per row
-
-__device__ __forceinline__ uint32_t row_max_u32(uint32_t v) {
-  v = max(v, (uint32_t)dpp<0xb1>((int)v, (int)v));
-  v = max(v, (uint32_t)dpp<0x4e>((int)v, (int)v));
-  v = max(v, (uint32_t)dpp<0x141>((int)v, (int)v));
-  v = max(v, (uint32_t)dpp<0x140>((int)v, (int)v));
-  return v;
-}
-
-// |x| of non-negative floats compares like its bit pattern
-__device__ __forceinline__ uint32_t abs_bits(float x) { return __float_as_uint(x) & 0x7fffffffu; }
 
 __device__ __forceinline__ uint32_t block_max_u32(uint32_t v, uint32_t* sh) {
   v = row_max_u32(v);
@@ -45,36 +36,6 @@ __device__ __forceinline__ uint32_t block_max_u32(uint32_t v, uint32_t* sh) {
   return r;
 }
 
-__device__ __forceinline__ float scale_of(uint32_t amax_bits) {
-  const float s = __fdiv_rn(__uint_as_float(amax_bits), E4M3_MAX);
-  return s > MIN_SCALE ? s : MIN_SCALE;
-}
-
-// quantize 8 values with one scale -> 8 e4m3 bytes
-__device__ __forceinline__ uint2 quant8(const float (&a)[8], float s) {
-  uint32_t w[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    float x0 = __fdiv_rn(a[2 * j], s), x1 = __fdiv_rn(a[2 * j + 1], s);
-    x0 = fminf(fmaxf(x0, -E4M3_MAX), E4M3_MAX);
-    x1 = fminf(fmaxf(x1, -E4M3_MAX), E4M3_MAX);
-    w[j] = f32x2_to_e4m3(x0, x1);
-  }
-  return make_uint2(w[0] | (w[1] << 16), w[2] | (w[3] << 16));
-}
-
-__device__ __forceinline__ void load8_bf16(const uint16_t* p, float (&v)[8]) {
-  const uint4 r = *reinterpret_cast<const uint4*>(p);
-  const uint32_t u[4] = {r.x, r.y, r.z, r.w};
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    v[2 * j] = __uint_as_float(u[j] << 16);
-    v[2 * j + 1] = __uint_as_float(u[j] & 0xffff0000u);
-  }
-}
-
-// group == 128: one scale per 128 columns; group == 0: one scale per row. K % 8 == 0 and, for
-// group 128, K % 128 == 0 (checked by the entry point).
 __global__ __launch_bounds__(QT) void group_quant_k(const uint16_t* __restrict__ x, int K,
                                                     int ldx, int group,
                                                     uint8_t* __restrict__ q,
@@ -100,21 +61,7 @@ __global__ __launch_bounds__(QT) void group_quant_k(const uint16_t* __restrict__
     }
     return;
   }
-  const int ng = K / 128;
-  for (int base = 0; base < K; base += QT * 8) {     // uniform trip count over the block
-    const int c = base + threadIdx.x * 8;
-    const bool in = c < K;
-    float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    if (in) load8_bf16(xr + c, v);
-    uint32_t m = 0;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) m = max(m, abs_bits(v[j]));
-    const float s = scale_of(row_max_u32(m));
-    if (in) {
-      *reinterpret_cast<uint2*>(qr + c) = quant8(v, s);
-      if ((threadIdx.x & 15) == 0) scale[(size_t)row * ng + c / 128] = s;
-    }
-  }
+  group_quant_row128(xr, K, qr, scale + (size_t)row * (K / 128));
 }
 
 // x [rows, 2d] bf16 (gate | up), ldx elements apart; q [rows, d]; scale [rows, d/group or 1];

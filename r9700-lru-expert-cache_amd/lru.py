@@ -110,6 +110,27 @@ def _r4d_lru_fused(topk_ids: torch.Tensor, table: torch.Tensor, map_cold: torch.
     check(rc, "r4d_lru_fused (E and slots must be <= 1024)")
 
 
+def _rlu_lru_fused_quant(topk_ids: torch.Tensor, state: list[torch.Tensor],
+                        out: list[torch.Tensor], max_distinct: int, max_inserts: int,
+                        block_size: int, x: torch.Tensor, q: torch.Tensor,
+                        scale: torch.Tensor) -> None:
+    """_r4d_lru_fused and, in the same launch, the per-token-group-128 e4m3 quant of x
+    [rows, K] bf16 into q [rows, K] / scale [rows, K/128] (no reference counterpart: the
+    reference launched the activation quant separately)."""
+    table, map_cold, slot_expert, slot_stamp, routed, step, miss, n_miss = state
+    _check_state(topk_ids, table, slot_expert, slot_stamp, routed, step, miss, n_miss)
+    assert max_inserts <= miss.shape[0]
+    assert x.dtype == torch.bfloat16 and x.stride(1) == 1 and q.is_contiguous()
+    rows, K = x.shape
+    rc = lib().rlu_lru_fused_quant(
+        _ptr(topk_ids), topk_ids.numel(), table.numel(), slot_expert.numel(), max_distinct,
+        max_inserts, _ptr(table), _ptr(map_cold), _ptr(slot_expert), _ptr(slot_stamp),
+        _ptr(routed), _ptr(step), _ptr(miss), _ptr(n_miss), block_size, out[0].numel(),
+        out[1].numel(), *[_ptr(o) for o in out], _ptr(x), rows, K, x.stride(0), _ptr(q),
+        _ptr(scale), _P(stream_ptr()))
+    check(rc, "rlu_lru_fused_quant")
+
+
 # ---- torch custom op registration (names and mutates_args of the reference) ---------------
 def _register():
     try:  # pragma: no cover - vLLM is not part of this image
@@ -223,4 +244,12 @@ class LruCache:
             out = self.alloc_align(ids.numel(), block_size)
         _r4d_lru_fused(ids, *self.state(), *out, self.max_distinct, self.max_inserts,
                        block_size)
+        return tuple(out[0:3]), tuple(out[3:6])
+
+    def fused_quant(self, topk_ids: torch.Tensor, out: list[torch.Tensor], x: torch.Tensor,
+                    q: torch.Tensor, scale: torch.Tensor, block_size: int = BLOCK):
+        """fused() plus the group-128 quant of x into (q, scale), one launch."""
+        ids = topk_ids.reshape(-1).to(torch.int32)
+        _rlu_lru_fused_quant(ids, self.state(), out, self.max_distinct, self.max_inserts,
+                             block_size, x, q, scale)
         return tuple(out[0:3]), tuple(out[3:6])

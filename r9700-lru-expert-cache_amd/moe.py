@@ -95,8 +95,15 @@ class LruMoELayer:
         self.tw = torch.empty((self.mtk,), dtype=torch.float32, device=dev)
 
     # -- _lru_step_fused: manager + both aligns in one launch, then the miss gather -----------
-    def _lru_step_fused(self, topk_ids: torch.Tensor, gather: bool, side: torch.cuda.Stream | None):
-        self.cache.fused(topk_ids, out=self.align, block_size=BLOCK)
+    def _lru_step_fused(self, topk_ids: torch.Tensor, gather: bool, side: torch.cuda.Stream | None,
+                        hidden_states: torch.Tensor | None = None):
+        """The fused manager + align; with hidden_states, the same launch also quantizes them
+        into (qx, xs) (the cache and the quant are independent and both feed GEMM1)."""
+        if hidden_states is None:
+            self.cache.fused(topk_ids, out=self.align, block_size=BLOCK)
+        else:
+            self.cache.fused_quant(topk_ids, self.align, hidden_states, self.qx, self.xs,
+                                   block_size=BLOCK)
         if not gather:
             return None
         # six-buffer ABI of the reference gather: the fp8 format has four per-expert buffers,
@@ -143,8 +150,7 @@ class LruMoELayer:
         topk_weights [M, top_k]."""
         M = hidden_states.shape[0]
         assert M == self.M and topk_ids.shape == (M, self.top_k)
-        waited = self._lru_step_fused(topk_ids, gather, side)
-        ops.fp8_quant_group(hidden_states, ops.GROUP, out=(self.qx, self.xs))
+        waited = self._lru_step_fused(topk_ids, gather, side, hidden_states)
         if waited is not None:
             torch.cuda.current_stream().wait_stream(waited)
         self._gemm_split(self.ic1, self.qx, self.xs, self.slots.w13, self.slots.s13,

@@ -16,6 +16,7 @@ import pytest
 
 from conftest import gpu_case
 from lru_cases import POLICY_SUITES, VICTIM_CASES, c1_trace, policy_start, victim_case
+from oracle import fp8
 from oracle import lru as olru
 
 torch = pytest.importorskip("torch")
@@ -339,3 +340,38 @@ def test_gather_rejects_bad_sizes(pkg):
         pkg._r4d_lru_gather([bad] * 6, [bad] * 6, m, nm, 8, 16)
     with pytest.raises(RuntimeError):
         pkg._r4d_lru_gather([d] * 6, [d] * 6, m, nm, 0, 16)
+
+
+@pytest.mark.parametrize("rows", [5, 20])
+def test_fused_quant_equals_fused_then_quant(pkg, rows):
+    """rlu_lru_fused_quant == r4d_lru_fused followed by rlu_quant_fp8_group(group 128), bit for
+    bit: cache state, both align outputs, e4m3 codes and scales."""
+    from importlib import import_module
+    ops = import_module(pkg.__name__ + ".ops")
+    ids_all, s = c1_trace()
+    rng = np.random.default_rng(rows)
+    E, S = 512, 257
+    a = pkg.LruCache.build(E, s.slot_expert.tolist(), None, DEV)
+    b = pkg.LruCache.build(E, s.slot_expert.tolist(), None, DEV)
+    for t, (sa, sb) in enumerate(zip(a.state(), b.state())):
+        sa.copy_(torch.from_numpy(np.ascontiguousarray(getattr(s, NAMES[t]))).to(DEV))
+        sb.copy_(sa)
+    x = torch.from_numpy(fp8.bf16_round(rng.standard_normal((rows, 2560)).astype(np.float32)
+                                        * 3)).to(torch.bfloat16).to(DEV)
+    for n in range(3):
+        ids = np.concatenate([ids_all[n + k % 4] for k in range(rows // 5)]).astype(np.int32)
+        idt = torch.from_numpy(ids).to(DEV)
+        oa, ob = a.alloc_align(ids.size), b.alloc_align(ids.size)
+        q1 = torch.empty((rows, 2560), dtype=torch.float8_e4m3fn, device=DEV)
+        s1 = torch.empty((rows, 20), dtype=torch.float32, device=DEV)
+        gpu_case(f"fused quant rows={rows} step {n}")
+        a.fused_quant(idt, oa, x, q1, s1)
+        b.fused(idt, out=ob)
+        q2, s2 = ops.fp8_quant_group(x, 128)
+        torch.cuda.synchronize()
+        for ta, tb in zip(a.state(), b.state()):
+            assert torch.equal(ta, tb)
+        for ta, tb in zip(oa, ob):
+            assert torch.equal(ta, tb)
+        assert torch.equal(q1.view(torch.uint8), q2.view(torch.uint8))
+        assert torch.equal(s1, s2)
