@@ -30,47 +30,16 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "gemm_common.h"
 #include "numerics.h"
 #include "rlu.h"
 #include "wave.h"
 
 namespace rlu {
 
-typedef int v8i __attribute__((ext_vector_type(8)));
-typedef float v4f __attribute__((ext_vector_type(4)));
-typedef unsigned int v4u __attribute__((ext_vector_type(4)));
-
 constexpr int GWV = 4;      // waves per workgroup
 constexpr int MAXKPW = 24;  // 128-deep K steps per wave (K / 128 / SKW)
 constexpr int XM = 8;       // 4 * XM >= MAXKPW + max ring depth - 1
-
-__device__ __forceinline__ v8i pack8(v4u lo, v4u hi) {
-  v8i r;
-  r[0] = lo.x; r[1] = lo.y; r[2] = lo.z; r[3] = lo.w;
-  r[4] = hi.x; r[5] = hi.y; r[6] = hi.z; r[7] = hi.w;
-  return r;
-}
-
-__device__ __forceinline__ v4f mfma_f8(v8i a, v8i b) {
-  // formats 0/0 = e4m3 x e4m3; E8M0 scale 127 = 2^0 on both operands
-  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, v4f{0.f, 0.f, 0.f, 0.f}, 0, 0,
-                                                          0, 127, 0, 127);
-}
-
-// One weight set with its align output; the split call passes two (resident slots + the
-// full expert tensor) and runs both block lists in one launch.
-struct WSet {
-  const uint8_t* wq;
-  const float* ws;
-  const int* sorted_ids;
-  const int* expert_ids;
-  const int* npad;
-};
-
-// Register ring depth: D steps of A (32 B) + NPW weight strips (32 B each) per lane.
-__host__ __device__ constexpr int ring_of(int npw) {
-  return npw == 1 ? 8 : npw == 2 ? 5 : npw == 4 ? 3 : 2;
-}
 
 template <int NPW, int SKW, bool DENSE>
 __global__ __launch_bounds__(GWV * WAVE) void moe_gemm_k(
@@ -287,23 +256,13 @@ int launch(int npw, int sk, int grid, hipStream_t st, const uint8_t* qx, const f
   return (int)hipGetLastError();
 }
 
-static int num_cus() {
-  static int n = 0;
-  if (!n) {
-    int dev = 0;
-    hipGetDevice(&dev);
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      n = 256;
-  }
-  return n;
-}
 
 // wv = 0: one workgroup per item group (the hardware dispatcher balances the CUs); otherwise a
 // persistent grid of wv workgroups per CU
 static int grid_for(int items, int sk, int wv) {
   const int ipg = GWV / sk;
   const int need = (items + ipg - 1) / ipg;
-  const int g = wv ? num_cus() * wv : need;
+  const int g = wv ? device_cus() * wv : need;
   return g < need ? g : (need > 0 ? need : 1);
 }
 

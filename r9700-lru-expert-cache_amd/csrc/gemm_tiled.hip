@@ -17,6 +17,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "gemm_common.h"
 #include "numerics.h"
 #include "rlu.h"
 #include "wave.h"
@@ -24,28 +25,12 @@
 namespace rlu {
 namespace tiled {
 
-typedef int v8i __attribute__((ext_vector_type(8)));
-typedef float v4f __attribute__((ext_vector_type(4)));
-typedef unsigned int v4u __attribute__((ext_vector_type(4)));
-
 constexpr int TMB = 8;           // 16-row blocks per tile
 constexpr int TBN = 256;         // columns per tile (16 strips of 16)
 constexpr int NSTRIP = TBN / 16;
 constexpr int NTHR = 512;        // 8 waves: 2 interleaved block sets x 4 column quarters
 constexpr int MAXNB = 8192;      // blocks the tile builder handles (L = 131072 sorted ids)
 constexpr int TB_THR = 1024;
-
-__device__ __forceinline__ v8i pack8(v4u lo, v4u hi) {
-  v8i r;
-  r[0] = lo.x; r[1] = lo.y; r[2] = lo.z; r[3] = lo.w;
-  r[4] = hi.x; r[5] = hi.y; r[6] = hi.z; r[7] = hi.w;
-  return r;
-}
-
-__device__ __forceinline__ v4f mfma_f8(v8i a, v8i b) {
-  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, v4f{0.f, 0.f, 0.f, 0.f}, 0, 0,
-                                                          0, 127, 0, 127);
-}
 
 // ---- tile list ---------------------------------------------------------------------------
 __global__ __launch_bounds__(TB_THR) void tiles_k(const int* __restrict__ eids,
@@ -243,17 +228,6 @@ __global__ __launch_bounds__(NTHR) void tiled_k(const uint8_t* __restrict__ qx,
   }
 }
 
-static int num_cus() {
-  static int n = 0;
-  if (!n) {
-    int dev = 0;
-    (void)hipGetDevice(&dev);
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      n = 256;
-  }
-  return n;
-}
-
 }  // namespace tiled
 }  // namespace rlu
 
@@ -280,7 +254,7 @@ int rlu_moe_gemm_fp8blk_tiled(const void* qx, const float* xs, const void* wq, c
   if (wv < 0 || wv > 16) return -5;
   if (mtk == 0) return 0;
   const int items = max_tiles * (N / TBN);
-  int grid = num_cus() * (wv ? wv : 2);
+  int grid = rlu::device_cus() * (wv ? wv : 2);
   if (grid > items) grid = items;
   const size_t lds = sizeof(Smem);
   if (topk_weights)

@@ -28,6 +28,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "gemm_common.h"
 #include "numerics.h"
 #include "rlu.h"
 #include "wave.h"
@@ -35,8 +36,6 @@
 namespace rlu {
 namespace w4 {
 
-typedef unsigned int v4u __attribute__((ext_vector_type(4)));
-typedef float v4f __attribute__((ext_vector_type(4)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
 constexpr int WAVES = 8;
@@ -183,17 +182,6 @@ __global__ __launch_bounds__(WAVES * WAVE) void gemv_k(const uint16_t* __restric
   }
 }
 
-static int num_cus() {
-  static int n = 0;
-  if (!n) {
-    int dev = 0;
-    (void)hipGetDevice(&dev);
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      n = 256;
-  }
-  return n;
-}
-
 }  // namespace w4
 }  // namespace rlu
 
@@ -211,12 +199,12 @@ int rlu_gemm_w4_m16(const void* x, int M, int K, const void* wq, const unsigned*
   const int ipg = WAVES / skw;
   const int nitems = N / (16 * SS);
   const int passes = (nitems + ipg - 1) / ipg;
-  int grid = num_cus() * (wv ? wv : 1);
+  int grid = rlu::device_cus() * (wv ? wv : 1);
   if (grid > passes) grid = passes;
   const size_t lds = (size_t)G * 256 * 16 + (size_t)WAVES * SS * 4 * rlu::WAVE * 4;
 #define RLU_W4(SK, GQ)                                                                        \
   hipLaunchKernelGGL((gemv_k<SK, GQ>), dim3(grid), dim3(WAVES * rlu::WAVE), lds, stream,       \
-                     (const uint16_t*)x, M, K, (const v4u*)wq, sz, (uint16_t*)y, N)
+                     (const uint16_t*)x, M, K, (const rlu::v4u*)wq, sz, (uint16_t*)y, N)
 #define RLU_W4_GQ(SK)                                                                         \
   switch (gq) {                                                                               \
     case 1: RLU_W4(SK, 1); break;                                                             \
