@@ -20,17 +20,14 @@
 // l * 16: every weight load instruction of a wave is 1 KB contiguous, and a strip's K range is
 // one contiguous run. Activations stay row-major (they are gathered by sorted_ids).
 //
-// Work split: an item is (one 16-row block, one tile of 16 * NPW columns). SKW waves of a
-// workgroup split the item's K range, each streaming its part through a ring of D register
-// stages (loads for step k + D are issued after the MFMAs of step k); their partial sums are
-// added in LDS in split order, so a given SKW is deterministic. The block's metadata (expert id
-// and its 16 sorted ids) comes through scalar loads, which the vector-memory counter does not
-// track, and the activation scales, pre-multiplied by the weight-block scale, are staged in
-// LDS: after the metadata the whole K range is in flight with no further round trip.
+// Work split: an item is (one 16-row block, one tile of 16 * NPW columns); SKW waves of a
+// workgroup split its K range (item_mma in gemm_item.h) and add their partial sums in LDS in
+// split order, so a given SKW is deterministic.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #include "gemm_common.h"
+#include "gemm_item.h"
 #include "numerics.h"
 #include "rlu.h"
 #include "wave.h"
@@ -38,22 +35,17 @@
 namespace rlu {
 
 constexpr int GWV = 4;      // waves per workgroup
-constexpr int MAXKPW = 24;  // 128-deep K steps per wave (K / 128 / SKW)
-constexpr int XM = 8;       // 4 * XM >= MAXKPW + max ring depth - 1
 
 template <int NPW, int SKW, bool DENSE>
 __global__ __launch_bounds__(GWV * WAVE) void moe_gemm_k(
     const uint8_t* __restrict__ qx, const float* __restrict__ xs, WSet s0, WSet s1, int nsets,
     uint16_t* __restrict__ y, const float* __restrict__ tw, int mtk, int top_k, int K, int N) {
-  constexpr int D = ring_of(NPW);
   constexpr int IPG = GWV / SKW;                    // items per workgroup pass
   extern __shared__ float lds[];                    // [GWV][nsteps][16] scales, then partials
   const int lane = lane_id();
   const int wv = uniform(threadIdx.x / WAVE);       // wave-uniform: item metadata in SGPRs
   const int sub = wv / SKW, ks = wv % SKW;
-  const int nkg = K / 128;
-  const int kpw = nkg / SKW;                        // K steps of this wave
-  const int nsteps = (kpw + D - 1) / D * D;         // padded to the ring; padding scales are 0
+  const int nsteps = item_steps<NPW, SKW>(K);
   const int NT = 16 * NPW;
   const int ntiles = N / NT;
   const int nb0 = DENSE ? 1 : (s0.npad[0] >> 4);
@@ -62,7 +54,7 @@ __global__ __launch_bounds__(GWV * WAVE) void moe_gemm_k(
   const int ngroups = (nitems + IPG - 1) / IPG;
   float* sx = lds + (size_t)wv * nsteps * 16;
   float* red = lds + (size_t)GWV * nsteps * 16;     // [2][GWV][NPW * 4][64]
-  const int r16 = lane & 15, c4 = lane >> 4;
+  const int r16 = lane & 15;
   int parity = 0;
 
   for (int grp = blockIdx.x; grp < ngroups; grp += gridDim.x, parity ^= 1) {
@@ -82,110 +74,11 @@ __global__ __launch_bounds__(GWV * WAVE) void moe_gemm_k(
     for (int s = 0; s < NPW; ++s) acc[s] = v4f{0.f, 0.f, 0.f, 0.f};
     int sod[4] = {mtk, mtk, mtk, mtk};
     float twv[4] = {1.f, 1.f, 1.f, 1.f};
-    if (live) {
-      // the block's 16 row ids (scalar loads), this lane's A row (operand layout) and the
-      // four output rows it holds (D layout: rows 4 c4 + i, column r16)
-      int so = DENSE ? r16 : mtk;
-      if (!DENSE) {
-        int ids[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) ids[i] = sids[b * 16 + i];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) so = r16 == i ? ids[i] : so;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          int v = ids[i];
-#pragma unroll
-          for (int c = 1; c < 4; ++c) v = c4 == c ? ids[4 * c + i] : v;
-          sod[i] = v;
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sod[i] = 4 * c4 + i;
-      }
-      if (tw && ks == 0) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) twv[i] = tw[sod[i] < mtk ? sod[i] : 0];
-      }
-      const bool valid = so < mtk;
-      const int arow = valid ? so / top_k : 0;
-      const int kg0 = ks * kpw;
-      // activation scale x weight-block scale for step k = 4 m + c4 of row r16; issued before
-      // the weight loads so that staging them waits for nothing else
-      const float* xrow = xs + (size_t)arow * nkg + kg0;
-      const float* wsr = ws + ((size_t)eid * (N / 128) + n0 / 128) * nkg + kg0;
-      float xv[XM], wv_[XM];
-#pragma unroll
-      for (int m = 0; m < XM; ++m) {
-        if (4 * m < nsteps) {                       // uniform; the product waits for the store
-          const int k = min(4 * m + c4, kpw - 1);
-          xv[m] = xrow[k];
-          wv_[m] = wsr[k];
-        }
-      }
-      const uint8_t* A = qx + (size_t)arow * K + kg0 * 128 + 16 * c4;
-      const uint8_t* W = wq + ((size_t)eid * N + n0) * K + (size_t)kg0 * 2048 + lane * 16;
-      v4u ra[D][2], rb[D][NPW][2];
-      auto issue = [&](int j, int k) {
-        ra[j][0] = *reinterpret_cast<const v4u*>(A + k * 128);
-        ra[j][1] = *reinterpret_cast<const v4u*>(A + k * 128 + 64);
-#pragma unroll
-        for (int s = 0; s < NPW; ++s) {
-          const v4u* p = reinterpret_cast<const v4u*>(W + (size_t)s * 16 * K + (size_t)k * 2048);
-          rb[j][s][0] = __builtin_nontemporal_load(p);
-          rb[j][s][1] = __builtin_nontemporal_load(p + 64);
-        }
-      };
-      auto step = [&](int j, int k) {
-        const v4f f = *reinterpret_cast<const v4f*>(sx + k * 16 + 4 * c4);
-        const v8i av = pack8(ra[j][0], ra[j][1]);
-#pragma unroll
-        for (int s = 0; s < NPW; ++s) {
-          const v4f d = mfma_f8(av, pack8(rb[j][s][0], rb[j][s][1]));
-#pragma unroll
-          for (int i = 0; i < 4; ++i) acc[s][i] = fmaf(d[i], f[i], acc[s][i]);
-        }
-      };
-#pragma unroll
-      for (int j = 0; j < D; ++j) issue(j, min(j, kpw - 1));
-#pragma unroll
-      for (int m = 0; m < XM; ++m) {
-        const int k = 4 * m + c4;
-        if (4 * m < nsteps && k < nsteps)
-          sx[k * 16 + r16] = (k < kpw && valid) ? xv[m] * wv_[m] : 0.f;
-      }
-      wave_lds_sync();
-      int c0 = 0;
-      for (; c0 + D < nsteps; c0 += D) {
-#pragma unroll
-        for (int j = 0; j < D; ++j) {
-          step(j, c0 + j);
-          issue(j, min(c0 + j + D, kpw - 1));
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < D; ++j) step(j, c0 + j);
-    }
-    if (SKW > 1) {
-      float* rbuf = red + (size_t)parity * GWV * NPW * 4 * WAVE;
-      if (ks > 0) {
-#pragma unroll
-        for (int s = 0; s < NPW; ++s)
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            rbuf[((size_t)wv * NPW * 4 + s * 4 + i) * WAVE + lane] = acc[s][i];
-      }
-      lds_barrier();
-      if (ks == 0) {
-#pragma unroll
-        for (int x = 1; x < SKW; ++x)
-#pragma unroll
-          for (int s = 0; s < NPW; ++s)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              acc[s][i] += rbuf[((size_t)(wv + x) * NPW * 4 + s * 4 + i) * WAVE + lane];
-      }
-    }
+    if (live)
+      item_mma<NPW, SKW, DENSE>(qx, xs, wq, ws, sids, eid, b, n0, tw, mtk, top_k, K, N, ks, sx,
+                                acc, sod, twv);
+    if (SKW > 1)
+      splitk_reduce<NPW, SKW>(acc, red + (size_t)parity * GWV * NPW * 4 * WAVE, wv, ks);
     if (live && ks == 0) {
       // epilogue: rows this lane holds, routed weight, bf16, only live rows
 #pragma unroll

@@ -1,0 +1,159 @@
+// One wave's share of one grouped-GEMM item, shared by the decode kernels (gemm.hip: plain bf16
+// output; gemm_act.hip: SiLU-mul-quant epilogue).
+//
+// An item is (one 16-row block, 16 * NPW output columns starting at n0). SKW waves split its K
+// range; wave ks streams steps [ks * kpw, (ks + 1) * kpw) of every strip through a ring of D
+// register stages: loads for step k + D are issued after the MFMAs of step k. The block's
+// metadata (expert id, 16 sorted ids) arrives through scalar loads, which the vector-memory
+// counter does not track, and the activation scale times the weight-block scale is staged per
+// step in LDS (sx), so after the metadata the whole K range is in flight with no further round
+// trip. The float32 block scales are applied per step in the accumulator,
+// acc += mfma * (xs * ws), the same association for every NPW at a given SKW.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "gemm_common.h"
+#include "numerics.h"
+#include "wave.h"
+
+namespace rlu {
+
+constexpr int MAXKPW = 24;  // 128-deep K steps per wave (K / 128 / SKW)
+constexpr int XM = 8;       // 4 * XM >= MAXKPW + max ring depth - 1
+
+// K steps of one wave, padded to the ring depth D (the padding steps carry zero scales)
+template <int NPW, int SKW, int D = ring_of(NPW)>
+__host__ __device__ __forceinline__ int item_steps(int K) {
+  const int kpw = K / 128 / SKW;
+  return (kpw + D - 1) / D * D;
+}
+
+// Accumulates this wave's K share of the item into acc (D layout: lane l holds rows
+// 4 (l / 16) + i, column l % 16 of each strip) and returns the item's row ids for those rows
+// (sod; mtk = padding) and, for wave ks == 0 when tw is given, their routed weights (twv).
+// sx: this wave's item_steps() x 16 floats of LDS. D: register ring depth.
+template <int NPW, int SKW, bool DENSE, int D = ring_of(NPW)>
+__device__ __forceinline__ void item_mma(const uint8_t* __restrict__ qx,
+                                         const float* __restrict__ xs,
+                                         const uint8_t* __restrict__ wq,
+                                         const float* __restrict__ ws,
+                                         const int* __restrict__ sids, int eid, int b, int n0,
+                                         const float* __restrict__ tw, int mtk, int top_k, int K,
+                                         int N, int ks, float* sx, v4f (&acc)[NPW],
+                                         int (&sod)[4], float (&twv)[4]) {
+  const int lane = lane_id();
+  const int r16 = lane & 15, c4 = lane >> 4;
+  const int nkg = K / 128;
+  const int kpw = nkg / SKW;
+  const int nsteps = item_steps<NPW, SKW, D>(K);
+  // the block's 16 row ids (scalar loads), this lane's A row (operand layout) and the four
+  // output rows it holds (D layout: rows 4 c4 + i, column r16)
+  int so = DENSE ? r16 : mtk;
+  if (!DENSE) {
+    int ids[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) ids[i] = sids[b * 16 + i];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) so = r16 == i ? ids[i] : so;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      int v = ids[i];
+#pragma unroll
+      for (int c = 1; c < 4; ++c) v = c4 == c ? ids[4 * c + i] : v;
+      sod[i] = v;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sod[i] = 4 * c4 + i;
+  }
+  if (tw && ks == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) twv[i] = tw[sod[i] < mtk ? sod[i] : 0];
+  }
+  const bool valid = so < mtk;
+  const int arow = valid ? so / top_k : 0;
+  const int kg0 = ks * kpw;
+  // activation scale x weight-block scale for step k = 4 m + c4 of row r16; issued before the
+  // weight loads so that staging them waits for nothing else
+  const float* xrow = xs + (size_t)arow * nkg + kg0;
+  const float* wsr = ws + ((size_t)eid * (N / 128) + n0 / 128) * nkg + kg0;
+  float xv[XM], wv_[XM];
+#pragma unroll
+  for (int m = 0; m < XM; ++m) {
+    if (4 * m < nsteps) {                           // uniform; the product waits for the store
+      const int k = min(4 * m + c4, kpw - 1);
+      xv[m] = xrow[k];
+      wv_[m] = wsr[k];
+    }
+  }
+  const uint8_t* A = qx + (size_t)arow * K + kg0 * 128 + 16 * c4;
+  const uint8_t* W = wq + ((size_t)eid * N + n0) * K + (size_t)kg0 * 2048 + lane * 16;
+  v4u ra[D][2], rb[D][NPW][2];
+  auto issue = [&](int j, int k) {
+    ra[j][0] = *reinterpret_cast<const v4u*>(A + k * 128);
+    ra[j][1] = *reinterpret_cast<const v4u*>(A + k * 128 + 64);
+#pragma unroll
+    for (int s = 0; s < NPW; ++s) {
+      const v4u* p = reinterpret_cast<const v4u*>(W + (size_t)s * 16 * K + (size_t)k * 2048);
+      rb[j][s][0] = __builtin_nontemporal_load(p);
+      rb[j][s][1] = __builtin_nontemporal_load(p + 64);
+    }
+  };
+  auto step = [&](int j, int k) {
+    const v4f f = *reinterpret_cast<const v4f*>(sx + k * 16 + 4 * c4);
+    const v8i av = pack8(ra[j][0], ra[j][1]);
+#pragma unroll
+    for (int s = 0; s < NPW; ++s) {
+      const v4f d = mfma_f8(av, pack8(rb[j][s][0], rb[j][s][1]));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[s][i] = fmaf(d[i], f[i], acc[s][i]);
+    }
+  };
+#pragma unroll
+  for (int j = 0; j < D; ++j) issue(j, min(j, kpw - 1));
+#pragma unroll
+  for (int m = 0; m < XM; ++m) {
+    const int k = 4 * m + c4;
+    if (4 * m < nsteps && k < nsteps)
+      sx[k * 16 + r16] = (k < kpw && valid) ? xv[m] * wv_[m] : 0.f;
+  }
+  wave_lds_sync();
+  int c0 = 0;
+  for (; c0 + D < nsteps; c0 += D) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      step(j, c0 + j);
+      issue(j, min(c0 + j + D, kpw - 1));
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < D; ++j) step(j, c0 + j);
+}
+
+// Split-K: waves ks > 0 of each item add their partial sums into wave ks == 0 through LDS, in
+// split order (deterministic). rbuf: nwaves x NPW x 4 x 64 floats; every wave of the workgroup
+// takes part (one LDS barrier).
+template <int NPW, int SKW>
+__device__ __forceinline__ void splitk_reduce(v4f (&acc)[NPW], float* rbuf, int wv, int ks) {
+  const int lane = lane_id();
+  if (ks > 0) {
+#pragma unroll
+    for (int s = 0; s < NPW; ++s)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        rbuf[((size_t)wv * NPW * 4 + s * 4 + i) * WAVE + lane] = acc[s][i];
+  }
+  lds_barrier();
+  if (ks == 0) {
+#pragma unroll
+    for (int x = 1; x < SKW; ++x)
+#pragma unroll
+      for (int s = 0; s < NPW; ++s)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          acc[s][i] += rbuf[((size_t)(wv + x) * NPW * 4 + s * 4 + i) * WAVE + lane];
+  }
+}
+
+}  // namespace rlu
