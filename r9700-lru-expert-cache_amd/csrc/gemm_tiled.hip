@@ -31,6 +31,7 @@ constexpr int NSTRIP = TBN / 16;
 constexpr int NTHR = 512;        // 8 waves: 2 interleaved block sets x 4 column quarters
 constexpr int MAXNB = 8192;      // blocks the tile builder handles (L = 131072 sorted ids)
 constexpr int TB_THR = 1024;
+constexpr int NXCD = 8;          // XCDs of an MI355X
 
 // ---- tile list ---------------------------------------------------------------------------
 __global__ __launch_bounds__(TB_THR) void tiles_k(const int* __restrict__ eids,
@@ -119,9 +120,16 @@ __global__ __launch_bounds__(NTHR) void tiled_k(const uint8_t* __restrict__ qx,
   const int r16 = lane & 15, c4 = lane >> 4;
   const int ncb = N / TBN;
   const int nkg = K / 128;
-  const int nitems = ntiles_p[0] * ncb;
+  // XCD-aware order: workgroups are dispatched round-robin over the XCDs, so workgroup b runs
+  // on XCD b % 8. Each XCD takes a contiguous range of tiles with all their column blocks, so
+  // a tile's gathered activation rows come into one L2 instead of one per column block.
+  const int nx = gridDim.x % NXCD == 0 ? NXCD : 1;
+  const int xcd = blockIdx.x % nx, per = gridDim.x / nx;
+  const int nt = ntiles_p[0];
+  const int i0 = (int)((long long)nt * xcd / nx) * ncb;
+  const int i1 = (int)((long long)nt * (xcd + 1) / nx) * ncb;
 
-  for (int item = blockIdx.x; item < nitems; item += gridDim.x) {
+  for (int item = i0 + blockIdx.x / nx; item < i1; item += per) {
     const int ti = item / ncb, cb = item - ti * ncb;
     const int b0 = tiles[2 * ti], nbk = tiles[2 * ti + 1];
     const int e = eids[b0];
@@ -256,6 +264,7 @@ int rlu_moe_gemm_fp8blk_tiled(const void* qx, const float* xs, const void* wq, c
   const int items = max_tiles * (N / TBN);
   int grid = rlu::device_cus() * (wv ? wv : 2);
   if (grid > items) grid = items;
+  if (grid >= NXCD) grid -= grid % NXCD;           // whole XCD rounds (see tiled_k)
   const size_t lds = sizeof(Smem);
   if (topk_weights)
     hipLaunchKernelGGL(tiled_k<true>, dim3(grid), dim3(NTHR), lds, stream, (const uint8_t*)qx,
