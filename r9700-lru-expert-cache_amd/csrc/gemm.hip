@@ -214,8 +214,12 @@ int rlu_moe_gemm_split(const void* qx, const float* xs, const void* wq_hot, cons
   if (rlu::bad_sk(K, sk)) return -4;
   if (wv < 0 || wv > 16) return -5;
   if (mtk == 0) return 0;
+  // live blocks are numbered densely (hot list, then cold list) and each holds at least one of
+  // the mtk rows, so there are at most min(2 ceil(em / 16), mtk) of them: the grid covers no
+  // more (workgroups past the live ones still cost a dispatch and a scalar load each)
   const int nb = (em + 15) / 16;
-  const int items = 2 * nb * (N / (16 * npw));
+  const int nblive = 2 * nb < mtk ? 2 * nb : mtk;
+  const int items = nblive * (N / (16 * npw));
   const int grid = rlu::grid_for(items, sk, wv);
   const rlu::WSet s0{(const uint8_t*)wq_hot, ws_hot, sorted_hot, eids_hot, npad_hot};
   const rlu::WSet s1{(const uint8_t*)wq, ws, sorted_cold, eids_cold, npad_cold};
