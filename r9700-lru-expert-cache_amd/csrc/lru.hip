@@ -5,11 +5,12 @@
 // lru_fused_k :418-575, lru_gather_k :271-301); the entry points at the bottom keep its C-ABI.
 // The implementation is this build's own, shaped for wave64 CDNA4:
 //
-//  * One workgroup of 256 threads (one wave per SIMD), five barriers for the fused kernel
+//  * One workgroup of 256 threads (one wave per SIMD), seven barriers for the fused kernel
 //    (three for the manager). Every global load is issued up front, so the kernel pays one
-//    memory round trip, not one per phase; the align outputs are pre-filled with their
-//    sentinels by coalesced stores in the same window, and only the first barrier waits for
-//    global stores (the rest order LDS only).
+//    memory round trip, not one per phase. Decode-sized align outputs are built in LDS and
+//    written once, coalesced, with the sentinels past num_post_pad written directly; larger
+//    ones are pre-filled with their sentinels in global memory, and only the first barrier
+//    waits for global stores (the rest order LDS only).
 //  * Cross-lane reductions and scans are DPP + v_readlane (wave-uniform scalars), not LDS
 //    shuffles.
 //  * Routed / non-resident sets are 64-bit-word bitmaps built from wave ballots; misses are
@@ -21,8 +22,9 @@
 //    themselves. Cost grows with key bits and nins, never with a per-insert block reduction,
 //    so there is no insert-count cliff.
 //  * Align is stable at every mk: a token's rank inside its bucket is the number of earlier
-//    tokens routed to the same expert, from a bit-sliced wave match plus per-wave counts in
-//    LDS.
+//    tokens routed to the same expert -- up to 256 tokens a popcount of the expert's token
+//    bitmap below it (each token places itself), above that a bit-sliced wave match plus
+//    per-wave counts in LDS.
 //
 // Preconditions (checked by the reference's own tests after every step, tests/lru/test_lru.py:
 // 138-145): table/map_cold complementary, table[slot_expert[s]] == s for resident slots,
@@ -64,7 +66,6 @@ struct LruLds {
   uint64_t vkey[MAXINS];             // victims, compacted, before ranking
   int vpack[MAXINS];                 // (slot << 16) | (old expert & 0xffff), same order
   int cnt_h[MAXS];                   // post-update tokens per hot bucket (slot)
-  int hexp[MAXS];                    // post-update expert of a hot bucket with tokens
   int cnt_c[MAXE];                   // post-update tokens per cold bucket (expert)
   int cum_h[MAXS];
   int cum_c[MAXE];
@@ -318,14 +319,14 @@ __device__ __forceinline__ void fill_align(int* __restrict__ oh, int* __restrict
   }
 }
 
-// The expert ids of a thread's buckets and, when `tokens`, each bucket's tokens in index
-// order (from the per-expert token masks).
+// The starts (cum_h / cum_c) and expert ids of a thread's buckets; with pad >= 0 also the
+// padding entries of each bucket, [start + count, start + padded count), set to pad.
 __device__ __forceinline__ void place_buckets(LruLds& L, int* __restrict__ oh,
                                               int* __restrict__ oc, int* __restrict__ eh,
                                               int* __restrict__ ec, const int (&ph)[EJ],
                                               const int (&pc)[EJ], int h0, int h1, int c0,
                                               int c1, int runa, int runb, int NB, const Blk& B,
-                                              bool tokens) {
+                                              int pad) {
 #pragma unroll
   for (int side = 0; side < 2; ++side) {
     const bool hs = side == 0;
@@ -344,24 +345,30 @@ __device__ __forceinline__ void place_buckets(LruLds& L, int* __restrict__ oh,
           int* eo = hs ? eh : ec;
           for (int k = B.blk(run); k < B.blk(run + B.pad(c)); ++k)
             if (k < NB) eo[k] = i;
-          if (tokens) {
+          if (pad >= 0) {
             int* so = hs ? oh : oc;
-            const int x = hs ? L.hexp[i] : i;
-            int p = run;
-#pragma unroll
-            for (int wd = 0; wd < TW; ++wd) {
-              uint64_t m = L.tk.tmask[x][wd];
-              while (m) {
-                so[p++] = wd * 64 + __ffsll((long long)m) - 1;
-                m &= m - 1;
-              }
-            }
+            for (int k = run + c; k < run + B.pad(c); ++k) so[k] = pad;
           }
         }
         run += B.pad(c);
       }
     }
   }
+}
+
+// The post-update bucket of routed expert e: its slot when resident on entry or inserted now
+// (the rank-mr miss takes victim slot vslot[mr]), else -1 (the cold list).
+__device__ __forceinline__ int post_slot(const LruLds& L, int e, int S, int nact) {
+  int s = L.tab[e];
+  if ((unsigned)s < (unsigned)S) return s;
+  if (nact > 0) {
+    const uint64_t mw = L.rbits[e >> 6] & L.nres[e >> 6];
+    if ((mw >> (e & 63)) & 1ull) {
+      const int mr = L.mpre[e >> 6] + __popcll(mw & ((1ull << (e & 63)) - 1ull));
+      if (mr < nact) return L.vslot[mr];
+    }
+  }
+  return -1;
 }
 
 // The per-token-group-128 quant of the layer's hidden state, run by workgroups 1.. of the fused
@@ -374,7 +381,9 @@ struct QuantJob {
   float* scale;
 };
 
-template <bool ALIGN>
+// BSC: the align block size as a compile-time constant (16, the size every decode call uses),
+// or 0 to take bs at run time
+template <bool ALIGN, int BSC = 0>
 __global__ __launch_bounds__(NT) void lru_k(
     const int* __restrict__ ids, int mk, int E, int S, int max_distinct, int max_inserts,
     int* __restrict__ table, int* __restrict__ map_cold, int* __restrict__ slot_expert,
@@ -426,7 +435,6 @@ __global__ __launch_bounds__(NT) void lru_k(
 #pragma unroll
         for (int x = 0; x < TW; ++x) L.tk.tmask[tok0][x] = 0;
       }
-      fill_align(L.stage_h, L.stage_c, L.stage_eh, L.stage_ec, Lsz, NB, mk);
     } else {
       reinterpret_cast<uint4*>(&L.tk.wcnt[0][0])[t] = make_uint4(0, 0, 0, 0);
       fill_align(sorted_hot, sorted_cold, eids_hot, eids_cold, Lsz, NB, mk);
@@ -542,10 +550,7 @@ __global__ __launch_bounds__(NT) void lru_k(
         }
       }
       const bool hot = r && (unsigned)post < (unsigned)S;
-      if (hot) {
-        L.cnt_h[post] = c;
-        L.hexp[post] = e;
-      }
+      if (hot) L.cnt_h[post] = c;
       L.cnt_c[e] = (r && !hot) ? c : 0;
       L.ecnt[e] = 0;  // general path: becomes the running per-expert base of the chunks
     }
@@ -559,7 +564,7 @@ __global__ __launch_bounds__(NT) void lru_k(
   lds_barrier();  // 4
 
   // ---- block-padded exclusive scans: thread t owns a contiguous run of slots and experts ---
-  const Blk B(bs);
+  const Blk B(BSC ? BSC : bs);
   const int Ch = (S + NT - 1) / NT, Ce = (E + NT - 1) / NT;
   const int h0 = t * Ch, h1 = min(h0 + Ch, S);
   const int c0 = t * Ce, c1 = min(c0 + Ce, E);
@@ -592,24 +597,44 @@ __global__ __launch_bounds__(NT) void lru_k(
     npad_hot[0] = tota;
     npad_cold[0] = totb;
   }
-  // bucket starts, expert ids, and (staged) the tokens of each bucket in index order
+  // bucket starts and expert ids (staged: also each bucket's padding entries)
   if (staged)
     place_buckets(L, L.stage_h, L.stage_c, L.stage_eh, L.stage_ec, ph, pc, h0, h1, c0, c1, runa,
-                  runb, NB, B, true);
+                  runb, NB, B, mk);
   else
     place_buckets(L, sorted_hot, sorted_cold, eids_hot, eids_cold, ph, pc, h0, h1, c0, c1, runa,
-                  runb, NB, B, false);
+                  runb, NB, B, -1);
   lds_barrier();  // 6
 
   if (staged) {
-    // ---- copy the staged outputs out, coalesced --------------------------------------------
+    // ---- each token places itself: its bucket's start plus the number of the bucket's tokens
+    // with a smaller index (the set bits of its expert's token mask below it), so every bucket
+    // lists its tokens in index order --------------------------------------------------------
+    if (v0) {
+      const int e = tok0;
+      int rank = __popcll(L.tk.tmask[e][t >> 6] & ((1ull << (t & 63)) - 1ull));
+#pragma unroll
+      for (int wd = 0; wd < TW; ++wd)
+        if (wd < (t >> 6)) rank += __popcll(L.tk.tmask[e][wd]);
+      const int s = post_slot(L, e, S, nact);
+      const int pos = (s >= 0 ? L.cum_h[s] : L.cum_c[e]) + rank;
+      if (pos < Lsz) {
+        if (s >= 0)
+          L.stage_h[pos] = t;
+        else
+          L.stage_c[pos] = t;
+      }
+    }
+    lds_barrier();  // 7
+    // ---- copy the staged outputs out, coalesced; past num_post_pad the sentinels ------------
+    const int nbh = B.blk(tota), nbc = B.blk(totb);
     for (int k = t; k < Lsz; k += NT) {
-      sorted_hot[k] = L.stage_h[k];
-      sorted_cold[k] = L.stage_c[k];
+      sorted_hot[k] = k < tota ? L.stage_h[k] : mk;
+      sorted_cold[k] = k < totb ? L.stage_c[k] : mk;
     }
     for (int k = t; k < NB; k += NT) {
-      eids_hot[k] = L.stage_eh[k];
-      eids_cold[k] = L.stage_ec[k];
+      eids_hot[k] = k < nbh ? L.stage_eh[k] : -1;
+      eids_cold[k] = k < nbc ? L.stage_ec[k] : -1;
     }
     return;
   }
@@ -646,18 +671,7 @@ __global__ __launch_bounds__(NT) void lru_k(
     if (v) {
       int rank = L.ecnt[e] + inrank;
       for (int ww = 0; ww < w; ++ww) rank += L.tk.wcnt[ww][e];
-      // post-update bucket of e: resident on entry, inserted now, or cold
-      int s = L.tab[e];
-      if ((unsigned)s >= (unsigned)S) {
-        s = -1;
-        if (nact > 0) {
-          const uint64_t mw = L.rbits[e >> 6] & L.nres[e >> 6];
-          if ((mw >> (e & 63)) & 1ull) {
-            const int mr = L.mpre[e >> 6] + __popcll(mw & ((1ull << (e & 63)) - 1ull));
-            if (mr < nact) s = L.vslot[mr];
-          }
-        }
-      }
+      const int s = post_slot(L, e, S, nact);
       if (s >= 0) {
         const int pos = L.cum_h[s] + rank;
         if (pos < Lsz) sorted_hot[pos] = i;
@@ -736,10 +750,11 @@ int r4d_lru_fused(const int* topk_ids, int mk, int E, int S, int max_distinct,
   if (E <= 0 || E > rlu::MAXE || S <= 0 || S > rlu::MAXS) return -1;
   if (bs <= 0 || L <= 0 || NB <= 0 || mk < 0) return -1;
   if (max_inserts < 0 || max_inserts > rlu::MAXINS) return -1;
-  hipLaunchKernelGGL(rlu::lru_k<true>, dim3(1), dim3(rlu::NT), 0, stream, topk_ids, mk, E, S,
-                     max_distinct, max_inserts, table, map_cold, slot_expert, slot_stamp,
-                     routed, step, miss, n_miss, bs, L, NB, sorted_hot, eids_hot, npad_hot,
-                     sorted_cold, eids_cold, npad_cold, rlu::QuantJob{});
+  auto k = bs == 16 ? rlu::lru_k<true, 16> : rlu::lru_k<true, 0>;
+  hipLaunchKernelGGL(k, dim3(1), dim3(rlu::NT), 0, stream, topk_ids, mk, E, S, max_distinct,
+                     max_inserts, table, map_cold, slot_expert, slot_stamp, routed, step, miss,
+                     n_miss, bs, L, NB, sorted_hot, eids_hot, npad_hot, sorted_cold, eids_cold,
+                     npad_cold, rlu::QuantJob{});
   return (int)hipGetLastError();
 }
 
@@ -758,8 +773,9 @@ int rlu_lru_fused_quant(const int* topk_ids, int mk, int E, int S, int max_disti
   if (max_inserts < 0 || max_inserts > rlu::MAXINS) return -1;
   if (rows < 0 || K <= 0 || ldx < K || (rows > 0 && (!x || !q || !scale))) return -1;
   if (K % 128 || ldx % 8) return -2;
-  hipLaunchKernelGGL(rlu::lru_k<true>, dim3(1 + rows), dim3(rlu::NT), 0, stream, topk_ids, mk,
-                     E, S, max_distinct, max_inserts, table, map_cold, slot_expert, slot_stamp,
+  auto k = bs == 16 ? rlu::lru_k<true, 16> : rlu::lru_k<true, 0>;
+  hipLaunchKernelGGL(k, dim3(1 + rows), dim3(rlu::NT), 0, stream, topk_ids, mk, E, S,
+                     max_distinct, max_inserts, table, map_cold, slot_expert, slot_stamp,
                      routed, step, miss, n_miss, bs, L, NB, sorted_hot, eids_hot, npad_hot,
                      sorted_cold, eids_cold, npad_cold,
                      rlu::QuantJob{(const uint16_t*)x, K, ldx, (uint8_t*)q, scale});
