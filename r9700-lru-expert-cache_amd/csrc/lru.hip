@@ -74,7 +74,8 @@ struct LruLds {
     uint64_t tmask[MAXE][TW];        // staged path: bit i of expert e = token i routes to e
     uint8_t wcnt[NW][MAXE];          // general path: tokens per (wave, expert) in a chunk
   } tk;
-  int stage_h[LSTAGE], stage_c[LSTAGE];
+  alignas(16) int stage_h[LSTAGE];   // 16-byte units for the fill and the copy-out
+  alignas(16) int stage_c[LSTAGE];
   int stage_eh[NBSTAGE], stage_ec[NBSTAGE];
 };
 
@@ -356,6 +357,11 @@ __device__ __forceinline__ void place_buckets(LruLds& L, int* __restrict__ oh,
   }
 }
 
+// both align outputs start on a 16-byte boundary (the copy-out then stores 16-byte units)
+static inline bool aligned16(const int* a, const int* b) {
+  return (((uintptr_t)a | (uintptr_t)b) & 15) == 0;
+}
+
 // The post-update bucket of routed expert e: its slot when resident on entry or inserted now
 // (the rank-mr miss takes victim slot vslot[mr]), else -1 (the cold list).
 __device__ __forceinline__ int post_slot(const LruLds& L, int e, int S, int nact) {
@@ -391,7 +397,7 @@ __global__ __launch_bounds__(NT) void lru_k(
     long long* __restrict__ step, int* __restrict__ miss, int* __restrict__ n_miss, int bs,
     int Lsz, int NB, int* __restrict__ sorted_hot, int* __restrict__ eids_hot,
     int* __restrict__ npad_hot, int* __restrict__ sorted_cold, int* __restrict__ eids_cold,
-    int* __restrict__ npad_cold, QuantJob qj) {
+    int* __restrict__ npad_cold, QuantJob qj, bool vec_out) {
   if (blockIdx.x > 0) {
     const int r = blockIdx.x - 1;
     group_quant_row128(qj.x + (size_t)r * qj.ldx, qj.K, qj.q + (size_t)r * qj.K,
@@ -597,11 +603,15 @@ __global__ __launch_bounds__(NT) void lru_k(
     npad_hot[0] = tota;
     npad_cold[0] = totb;
   }
-  // bucket starts and expert ids (staged: also each bucket's padding entries)
-  if (staged)
+  // bucket starts and expert ids; staged: every entry below num_post_pad starts as the
+  // sentinel (the tokens overwrite theirs after the barrier)
+  if (staged) {
+    const int4 m4 = make_int4(mk, mk, mk, mk);
+    for (int k = 4 * t; k < tota; k += 4 * NT) *reinterpret_cast<int4*>(&L.stage_h[k]) = m4;
+    for (int k = 4 * t; k < totb; k += 4 * NT) *reinterpret_cast<int4*>(&L.stage_c[k]) = m4;
     place_buckets(L, L.stage_h, L.stage_c, L.stage_eh, L.stage_ec, ph, pc, h0, h1, c0, c1, runa,
-                  runb, NB, B, mk);
-  else
+                  runb, NB, B, -1);
+  } else
     place_buckets(L, sorted_hot, sorted_cold, eids_hot, eids_cold, ph, pc, h0, h1, c0, c1, runa,
                   runb, NB, B, -1);
   lds_barrier();  // 6
@@ -628,7 +638,22 @@ __global__ __launch_bounds__(NT) void lru_k(
     lds_barrier();  // 7
     // ---- copy the staged outputs out, coalesced; past num_post_pad the sentinels ------------
     const int nbh = B.blk(tota), nbc = B.blk(totb);
-    for (int k = t; k < Lsz; k += NT) {
+    int k0 = 0;
+    if (vec_out) {                                  // 16-byte stores (outputs 16-byte aligned)
+      for (int k = 4 * t; k + 4 <= Lsz; k += 4 * NT) {
+        // LDS read first, then a value select (a select of the source would become a generic
+        // load from LDS or from a private copy of the sentinel)
+        const int4 h = *reinterpret_cast<const int4*>(&L.stage_h[k]);
+        const int4 c = *reinterpret_cast<const int4*>(&L.stage_c[k]);
+        const bool ih = k < tota, ic = k < totb;
+        *reinterpret_cast<int4*>(sorted_hot + k) =
+            make_int4(ih ? h.x : mk, ih ? h.y : mk, ih ? h.z : mk, ih ? h.w : mk);
+        *reinterpret_cast<int4*>(sorted_cold + k) =
+            make_int4(ic ? c.x : mk, ic ? c.y : mk, ic ? c.z : mk, ic ? c.w : mk);
+      }
+      k0 = Lsz & ~3;
+    }
+    for (int k = k0 + t; k < Lsz; k += NT) {
       sorted_hot[k] = k < tota ? L.stage_h[k] : mk;
       sorted_cold[k] = k < totb ? L.stage_c[k] : mk;
     }
@@ -736,7 +761,7 @@ int r4d_lru_manage(const int* topk_ids, int mk, int E, int S, int max_distinct,
   hipLaunchKernelGGL(rlu::lru_k<false>, dim3(1), dim3(rlu::NT), 0, stream, topk_ids, mk, E, S,
                      max_distinct, max_inserts, table, map_cold, slot_expert, slot_stamp,
                      routed, step, miss, n_miss, 1, 0, 0, nullptr, nullptr, nullptr, nullptr,
-                     nullptr, nullptr, rlu::QuantJob{});
+                     nullptr, nullptr, rlu::QuantJob{}, false);
   return (int)hipGetLastError();
 }
 
@@ -754,7 +779,7 @@ int r4d_lru_fused(const int* topk_ids, int mk, int E, int S, int max_distinct,
   hipLaunchKernelGGL(k, dim3(1), dim3(rlu::NT), 0, stream, topk_ids, mk, E, S, max_distinct,
                      max_inserts, table, map_cold, slot_expert, slot_stamp, routed, step, miss,
                      n_miss, bs, L, NB, sorted_hot, eids_hot, npad_hot, sorted_cold, eids_cold,
-                     npad_cold, rlu::QuantJob{});
+                     npad_cold, rlu::QuantJob{}, rlu::aligned16(sorted_hot, sorted_cold));
   return (int)hipGetLastError();
 }
 
@@ -778,7 +803,8 @@ int rlu_lru_fused_quant(const int* topk_ids, int mk, int E, int S, int max_disti
                      max_distinct, max_inserts, table, map_cold, slot_expert, slot_stamp,
                      routed, step, miss, n_miss, bs, L, NB, sorted_hot, eids_hot, npad_hot,
                      sorted_cold, eids_cold, npad_cold,
-                     rlu::QuantJob{(const uint16_t*)x, K, ldx, (uint8_t*)q, scale});
+                     rlu::QuantJob{(const uint16_t*)x, K, ldx, (uint8_t*)q, scale},
+                     rlu::aligned16(sorted_hot, sorted_cold));
   return (int)hipGetLastError();
 }
 
