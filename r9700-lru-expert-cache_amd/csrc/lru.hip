@@ -158,8 +158,7 @@ __device__ __forceinline__ int select_victims(LruLds& L, int S, int nins, const 
         mx = x > mx ? x : mx;
       }
     }
-    mn = (uint32_t)(~wave_reduce64(~(uint64_t)mn, OpMax64()) );   // min via max of complement
-    mx = (uint32_t)wave_reduce64((uint64_t)mx, OpMax64());
+    wave_minmax_u32(mn, mx);
     uint64_t g[Q];
     int cnt0 = 0;
 #pragma unroll

@@ -76,6 +76,25 @@ __device__ __forceinline__ uint64_t wave_reduce64(uint64_t v, Op op) {  // wave-
   return op(r, readlane64(v, 48));
 }
 
+// unsigned minimum and maximum over the wave, both at once (wave-uniform results)
+__device__ __forceinline__ void wave_minmax_u32(uint32_t& mn, uint32_t& mx) {
+#define RLU_MM(C)                                            \
+  {                                                          \
+    const uint32_t a = (uint32_t)dpp<C>((int)mn, (int)mn);   \
+    const uint32_t b = (uint32_t)dpp<C>((int)mx, (int)mx);   \
+    mn = a < mn ? a : mn;                                    \
+    mx = b > mx ? b : mx;                                    \
+  }
+  RLU_MM(0xb1) RLU_MM(0x4e) RLU_MM(0x141) RLU_MM(0x140)
+#undef RLU_MM
+  const uint32_t n0 = (uint32_t)readlane((int)mn, 0), n1 = (uint32_t)readlane((int)mn, 16);
+  const uint32_t n2 = (uint32_t)readlane((int)mn, 32), n3 = (uint32_t)readlane((int)mn, 48);
+  const uint32_t x0 = (uint32_t)readlane((int)mx, 0), x1 = (uint32_t)readlane((int)mx, 16);
+  const uint32_t x2 = (uint32_t)readlane((int)mx, 32), x3 = (uint32_t)readlane((int)mx, 48);
+  mn = min(min(n0, n1), min(n2, n3));
+  mx = max(max(x0, x1), max(x2, x3));
+}
+
 __device__ __forceinline__ int row_sum(int v) {
   v += dpp<0xb1>(v, v);
   v += dpp<0x4e>(v, v);
