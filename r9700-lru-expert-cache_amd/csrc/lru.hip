@@ -260,10 +260,10 @@ __device__ __forceinline__ int select_victims(LruLds& L, int S, int nins, const 
   return nact;
 }
 
-// Wave 0 after the routed set is known: refresh the stamps of hit slots, then pick victims.
+// Wave 0 after the routed set is known: pick the victims among the slots whose expert is not
+// routed (the other waves refresh the hit stamps meanwhile).
 template <int Q>
 __device__ __forceinline__ int wave0_slots(LruLds& L, int S, int nins, bool ins_ok,
-                                           long long st, long long* __restrict__ slot_stamp,
                                            const int (&se)[QS], const long long (&sst)[QS]) {
   const int lane = lane_id();
   uint64_t sb[Q];
@@ -273,20 +273,17 @@ __device__ __forceinline__ int wave0_slots(LruLds& L, int S, int nins, bool ins_
 #pragma unroll
   for (int q = 0; q < Q; ++q) {
     const int i = lane + WAVE * q;
-    const bool busy = i < S && ((sb[q] >> lane) & 1ull);
-    if (ins_ok && busy) slot_stamp[i] = st;   // hit: r4d_lru.hip:228-238
-    ev[q] = i < S && !busy;
+    ev[q] = i < S && !((sb[q] >> lane) & 1ull);
   }
   if (!ins_ok || nins == 0) return 0;
   return select_victims<Q>(L, S, nins, se, sst, ev);
 }
 
 __device__ __forceinline__ int wave0_dispatch(LruLds& L, int S, int nins, bool ins_ok,
-                                              long long st, long long* __restrict__ slot_stamp,
                                               const int (&se)[QS], const long long (&sst)[QS]) {
   switch ((S + WAVE - 1) / WAVE) {
 #define RLU_Q(n) \
-  case n: return wave0_slots<n>(L, S, nins, ins_ok, st, slot_stamp, se, sst);
+  case n: return wave0_slots<n>(L, S, nins, ins_ok, se, sst);
     RLU_Q(1) RLU_Q(2) RLU_Q(3) RLU_Q(4) RLU_Q(5) RLU_Q(6) RLU_Q(7) RLU_Q(8)
     RLU_Q(9) RLU_Q(10) RLU_Q(11) RLU_Q(12) RLU_Q(13) RLU_Q(14) RLU_Q(15) RLU_Q(16)
 #undef RLU_Q
@@ -354,6 +351,15 @@ __device__ __forceinline__ void place_buckets(LruLds& L, int* __restrict__ oh,
       }
     }
   }
+}
+
+// tokens routed to expert e this step: its token bitmap (staged) or the atomic counts
+__device__ __forceinline__ int expert_tokens(const LruLds& L, int e, bool staged) {
+  if (!staged) return L.ecnt[e];
+  int c = 0;
+#pragma unroll
+  for (int x = 0; x < TW; ++x) c += __popcll(L.tk.tmask[e][x]);
+  return c;
 }
 
 // both align outputs start on a 16-byte boundary (the copy-out then stores 16-byte units)
@@ -491,7 +497,9 @@ __global__ __launch_bounds__(NT) void lru_k(
   }
   lds_barrier();  // 2
 
-  // ---- wave 0: distinct count, miss ranks, stamp refresh, victims --------------------------
+  // ---- wave 0: distinct count, miss ranks, victims; the other waves meanwhile do what does
+  // not depend on the victims: hit stamps, routed flags, bucket counts of every expert that
+  // is not a miss --------------------------------------------------------------------------
   if (w == 0) {
     uint64_t rw = 0, nw = 0;
     if (lane < NWORD) {
@@ -505,10 +513,29 @@ __global__ __launch_bounds__(NT) void lru_k(
     if (lane < NWORD) L.mpre[lane] = mincl - mpop;
     const bool ins_ok = distinct <= max_distinct;
     const int nins = ins_ok ? (total < max_inserts ? total : max_inserts) : 0;
-    const int nact = wave0_dispatch(L, S, nins, ins_ok, st, slot_stamp, se, sst);
+    const int nact = wave0_dispatch(L, S, nins, ins_ok, se, sst);
     if (lane == 0) {
       L.misc[0] = nact;
       L.misc[1] = nins;
+    }
+  } else {
+    const uint64_t rw = lane < NWORD ? L.rbits[lane] : 0ull;
+    const bool ins_ok = readlane(row_sum(__popcll(rw)), 0) <= max_distinct;
+    if (ins_ok) {                                    // hit: r4d_lru.hip:228-238
+      for (int i = t - WAVE; i < S; i += NT - WAVE)
+        if (bit_of(L.sbusy, i)) slot_stamp[i] = st;
+    }
+    for (int e = t - WAVE; e < E; e += NT - WAVE) {
+      const bool r = bit_of(L.rbits, e);
+      routed[e] = r ? 1 : 0;
+      const int s0 = L.tab[e];
+      if (ALIGN && !(r && s0 < 0)) {
+        const int c = r ? expert_tokens(L, e, staged) : 0;
+        const bool hot = r && (unsigned)s0 < (unsigned)S;
+        if (hot) L.cnt_h[s0] = c;
+        L.cnt_c[e] = (r && !hot) ? c : 0;
+        L.ecnt[e] = 0;  // general path: becomes the running per-expert base of the chunks
+      }
     }
   }
   lds_barrier();  // 3
@@ -516,16 +543,14 @@ __global__ __launch_bounds__(NT) void lru_k(
   const int nact = L.misc[0];
   const int nins = L.misc[1];
 
-  // ---- expert side: routed flags, miss list, installs, post-update bucket counts ----------
+  // ---- misses: miss list, installs, post-update bucket counts ------------------------------
 #pragma unroll
   for (int j = 0; j < EJ; ++j) {
     const int e = t + NT * j;
     if (e >= E) continue;
-    const bool r = bit_of(L.rbits, e);
-    routed[e] = r ? 1 : 0;
-    const bool ismiss = r && tab[j] < 0;
-    int post = tab[j];
-    if (ismiss && nins > 0) {
+    if (!(tab[j] < 0 && bit_of(L.rbits, e))) continue;
+    int post = -1;
+    if (nins > 0) {
       const uint64_t mw = L.rbits[e >> 6] & L.nres[e >> 6];
       const int rank = L.mpre[e >> 6] + __popcll(mw & ((1ull << (e & 63)) - 1ull));
       if (rank < nins) miss[2 * rank] = e;
@@ -545,19 +570,11 @@ __global__ __launch_bounds__(NT) void lru_k(
       }
     }
     if (ALIGN) {
-      int c = 0;
-      if (r) {
-        if (staged) {
-#pragma unroll
-          for (int x = 0; x < TW; ++x) c += __popcll(L.tk.tmask[e][x]);
-        } else {
-          c = L.ecnt[e];
-        }
-      }
-      const bool hot = r && (unsigned)post < (unsigned)S;
+      const int c = expert_tokens(L, e, staged);
+      const bool hot = (unsigned)post < (unsigned)S;
       if (hot) L.cnt_h[post] = c;
-      L.cnt_c[e] = (r && !hot) ? c : 0;
-      L.ecnt[e] = 0;  // general path: becomes the running per-expert base of the chunks
+      L.cnt_c[e] = hot ? 0 : c;
+      L.ecnt[e] = 0;
     }
   }
   if (t == 0) {
