@@ -10,6 +10,7 @@ from ._lib import LIB_PATH, LibraryMissing, lib  # noqa: F401
 from .lru import (LruCache, _align_sizes, _r4d_lru_fused, _r4d_lru_gather,  # noqa: F401
                   _r4d_lru_manage)
 from . import ops  # noqa: F401
+from . import hot_profile  # noqa: F401
 from . import traces  # noqa: F401
 from . import w4  # noqa: F401
 from .moe import ExpertWeights, LruMoELayer  # noqa: F401

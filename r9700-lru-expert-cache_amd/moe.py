@@ -49,6 +49,10 @@ class ExpertWeights:
     def tensors(self):
         return [self.w13, self.s13, self.w2, self.s2]
 
+    def per_expert_bytes(self) -> int:
+        """Bytes one expert occupies in the four buffers (what one slot costs in HBM)."""
+        return sum(t[0].numel() * t.element_size() for t in self.tensors())
+
     def ptrs(self) -> list[int]:
         """Device-visible addresses (pinned host tensors are translated)."""
         return [device_ptr_of_pinned(t) if t.is_pinned() else t.data_ptr()
@@ -93,6 +97,21 @@ class LruMoELayer:
         self.s2 = torch.empty((self.mtk, self.I // 128), dtype=torch.float32, device=dev)
         self.ic3 = torch.empty((self.mtk, self.H), dtype=torch.bfloat16, device=dev)
         self.tw = torch.empty((self.mtk,), dtype=torch.float32, device=dev)
+
+    @classmethod
+    def from_profile(cls, full: ExpertWeights, profile, layer: int, budget_gb: float,
+                     max_tokens: int, top_k: int, device="cuda", **kw) -> "LruMoELayer":
+        """The layer's warm start from a hot profile (hot_profile.HotProfile): its share of the
+        global budget_gb water-fill as the slots (r4d_mxfp4_moe.py.lru.diff:502-541 with
+        hot_ids_for_layer / profile_rank_for_layer), stamps by profile rank. Raises
+        ValueError when the layer is not profiled or gets no slot."""
+        from . import hot_profile as hp
+        sets = hp.hot_sets(profile, full.per_expert_bytes(), budget_gb)
+        if layer not in sets:
+            raise ValueError(f"layer {layer} is not in the hot profile")
+        if not sets[layer]:
+            raise ValueError(f"the {budget_gb} GB budget leaves layer {layer} no slot")
+        return cls(full, sets[layer], profile.rank(layer), max_tokens, top_k, device, **kw)
 
     # -- _lru_step_fused: manager + both aligns in one launch, then the miss gather -----------
     def _lru_step_fused(self, topk_ids: torch.Tensor, gather: bool, side: torch.cuda.Stream | None,

@@ -12,6 +12,7 @@ permutation and its drift. All draws come from one numpy PCG64 stream, in this o
             pos = rng.choice(E, reshuffle, replace=False); perm[pos] = perm[rng.permutation(pos)]
         for each row: perm[rng.choice(E, k, replace=False, p=p)]
 warm_hot(): the initial hot set = the S hottest of the initial permutation, with its ranks.
+profile_trace(): rows drawn from one layer's routing counts of a hot profile (hot_profile.py).
 
 layer_trace(): the many-layer step harness's routing: one zipf_trace per layer, seed
 base + layer, exponent `s` and `corr` tuned so that the cache sees the insert rate a real
@@ -87,3 +88,21 @@ def insert_storm_ids(rng: np.random.Generator, hot: np.ndarray, E: int, mk: int,
         routed = np.concatenate([routed, rng.choice(routed, mk - len(routed))])
     rng.shuffle(routed)
     return routed[:mk].astype(np.int32)
+
+
+def profile_trace(ranked: np.ndarray, counts: np.ndarray, E: int, seed: int = 0, rows: int = 20,
+                  k: int = 10, steps: int = 64) -> np.ndarray:
+    """A routing trace whose per-expert frequencies follow one layer of a hot profile: each
+    row draws k distinct experts without replacement with p(e) proportional to the layer's
+    routing count of e (experts the profile never saw are never drawn). One numpy PCG64
+    stream. -> ids int32 [steps, rows * k]."""
+    p = np.zeros(E, np.float64)
+    p[np.asarray(ranked, np.int64)] = np.asarray(counts, np.float64)
+    if (p > 0).sum() < k:
+        raise ValueError("the profile layer routes fewer than k experts")
+    p /= p.sum()
+    rng = np.random.default_rng(seed)
+    out = np.empty((steps, rows * k), np.int32)
+    for n in range(steps):
+        out[n] = np.concatenate([rng.choice(E, k, replace=False, p=p) for _ in range(rows)])
+    return out
