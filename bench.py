@@ -12,7 +12,9 @@ with routed weights, moe_sum -- captured once as a HIP graph and replayed with n
 
 `value` is ms per 52-layer step with every input resident in HBM: the miss gather, which reads
 pinned host memory over PCIe, is timed in a second graph and reported as
-`e2e_with_gather_ms_per_step`; the same step at B=1 (5 tokens) is `b1_ms_per_step`.
+`e2e_with_gather_ms_per_step`; the same step at B=1 (5 tokens) is `b1_ms_per_step`. The
+static hot/cold arm (inserts disabled: the warm-start set stays resident and every other
+routed expert is read over PCIe by the GEMMs, every step) is `e2e_static_arm_ms_per_step`.
 
     python bench.py [--steps K] [--warmup W] [--only-b4]
 """
@@ -84,7 +86,8 @@ def layer_trace(layer, rows, steps):
                             corr=corr)
 
 
-def build(torch, pkg, rows, steps, dev, pool_dev, host_full, layers_cache=None):
+def build(torch, pkg, rows, steps, dev, pool_dev, host_full, layers_cache=None,
+          max_inserts=None):
     """Layers (slots shared between batch sizes: the hot set depends only on the layer seed)."""
     trace = pkg.traces
     ids = np.empty((steps, LAYERS, rows, TOPK), np.int32)
@@ -99,7 +102,8 @@ def build(torch, pkg, rows, steps, dev, pool_dev, host_full, layers_cache=None):
             idx = torch.tensor(sorted(hot.tolist()), dtype=torch.int64, device=dev)
             slots = pkg.ExpertWeights(*[pool_dev[n].index_select(0, idx).contiguous()
                                         for n in ("w13", "w13s", "w2", "w2s")])
-        layers.append(pkg.LruMoELayer(host_full, hot, rank, rows, TOPK, dev, slots=slots))
+        layers.append(pkg.LruMoELayer(host_full, hot, rank, rows, TOPK, dev, slots=slots,
+                                      max_inserts=max_inserts))
     return layers, ids
 
 
@@ -593,6 +597,23 @@ def main():
         out["misses_per_layer_last_step"] = round(float(np.mean(nm)), 2)
         log(f"B=4 with PCIe miss gather: {mse:.3f} ms")
         del gA, gB
+        torch.cuda.synchronize()
+        # A/B control: the static hot/cold arm (inserts disabled: the warm-start set stays
+        # resident, every other routed expert is read over PCIe by the GEMMs, every step)
+        layersS, _ = build(torch, pkg, rows4, 1, dev, None, host_full, layers_cache=layers4,
+                           max_inserts=0)
+        gS = capture(torch, layersS, ids4_static, tw4, hb4, gather=True, side=side)
+        run_steps(torch, gS, ids4_dev, ids4_static, 0, 1)
+        mss, _ = time_steps(torch, gS, ids4_dev, ids4_static, 1, args.steps)
+        out["e2e_static_arm_ms_per_step"] = round(mss, 3)
+        # what that arm reads over PCIe: routed experts outside each layer's warm-start set
+        hots = [set(pkg.traces.warm_hot(layer_trace(l, rows4, 1)[1], S)[0].tolist())
+                for l in range(LAYERS)]
+        cold = [len(set(ids4[t_, l].ravel().tolist()) - hots[l])
+                for t_ in range(1, 1 + args.steps) for l in range(LAYERS)]
+        out["static_arm_cold_experts_per_layer"] = round(float(np.mean(cold)), 2)
+        log(f"B=4 static hot/cold arm (no inserts): {mss:.3f} ms")
+        del gS, layersS
         torch.cuda.synchronize()
         # B=1: same layers' slots, fresh caches, 5 tokens
         rows1 = 5

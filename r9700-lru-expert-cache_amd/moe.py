@@ -62,10 +62,14 @@ class ExpertWeights:
 class LruMoELayer:
     def __init__(self, full: ExpertWeights, hot_ids, rank: dict | None, max_tokens: int,
                  top_k: int, device="cuda", slots: ExpertWeights | None = None,
-                 npw1: int = 2, npw2: int = 4, sk1: int = 2, sk2: int = 1, wv: int = 0):
+                 npw1: int = 2, npw2: int = 4, sk1: int = 2, sk2: int = 1, wv: int = 0,
+                 max_inserts: int | None = None):
         """npw / sk: 16-column tiles per item and K split of gate_up (1) and down (2); the
         defaults are the fastest measured at the decode shapes (hidden 2560, intermediate
-        768, 5-20 tokens)."""
+        768, 5-20 tokens). max_inserts: cap on cache inserts per step (default
+        VLLM_R4D_LRU_MAX_INSERTS, 64); 0 is the static hot/cold arm -- the warm-start set stays
+        resident and every other routed expert is read from the full tensor
+        (r4d_mxfp4_moe.py.static.diff, and the README's MAX_INSERTS=0 ablation)."""
         dev = torch.device(device)
         self.full = full
         self.full_ptrs = full.ptrs()
@@ -87,7 +91,8 @@ class LruMoELayer:
             slots = ExpertWeights(*[t.index_select(0, idx.to(t.device)).to(dev).contiguous()
                                     for t in full.tensors()])
         self.slots = slots
-        self.cache = LruCache.build(self.E, hot, rank, dev)
+        self.cache = (LruCache.build(self.E, hot, rank, dev) if max_inserts is None else
+                      LruCache.build(self.E, hot, rank, dev, max_inserts=max_inserts))
         # align outputs and intermediates for exactly max_tokens rows
         self.align = self.cache.alloc_align(self.mtk, BLOCK)
         self.qx = torch.empty((self.M, self.H), dtype=ops.FP8, device=dev)

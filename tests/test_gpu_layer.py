@@ -116,3 +116,40 @@ def test_layer_steps_vs_oracle(pkg, pool, M):
         err = ogemm.rel_err(got, ref)
         assert err <= TOL, f"step {t}: rel err {err:.3e}"
     assert total_miss > 0, "the trace must exercise the miss path"
+
+
+def test_layer_static_arm(pkg, pool):
+    """max_inserts = 0 (the static hot/cold arm, r4d_mxfp4_moe.py.static.diff; the README's
+    MAX_INSERTS=0 ablation): no insert ever, the warm-start set stays in its slots, every
+    other routed expert is computed from the full tensor; state (stamps, step) and output
+    match the oracle with the same cap."""
+    M, steps = 5, 3
+    tr, perm0 = trace.zipf_trace(seed=55, E=E, rows=M, k=TOPK, steps=steps, s=1.1)
+    ids_all = tr.reshape(steps, M, TOPK).astype(np.int32)
+    hot, rank = trace.warm_hot(perm0, S)
+    full = pkg.ExpertWeights(pool["w13"], pool["w13s"], pool["w2"], pool["w2s"])
+    layer = pkg.LruMoELayer(full, hot, rank, M, TOPK, DEV, max_inserts=0)
+    st = olru.warm_start(E, S, hot, rank, max_inserts=0)
+    se0 = layer.cache.slot_expert.cpu().numpy().copy()
+    rng = np.random.default_rng(55)
+    cold_rows = 0
+    for t in range(steps):
+        ids = ids_all[t]
+        cold_rows += int((~np.isin(ids, hot)).sum())
+        x = fp8.bf16_round(rng.standard_normal((M, H)).astype(np.float32))
+        tw = rng.random((M, TOPK)).astype(np.float32)
+        out = torch.empty((M, H), dtype=torch.bfloat16, device=DEV)
+        gpu_case(f"static arm step {t}")
+        layer.apply(out, torch.from_numpy(x).to(torch.bfloat16).to(DEV),
+                    torch.from_numpy(tw).to(DEV), torch.from_numpy(ids).to(DEV), gather=True)
+        torch.cuda.synchronize()
+        olru.fused(st, ids.reshape(-1), 16)
+        for name, got in zip(olru.LruState.NAMES, layer.cache.state()):
+            if name == "routed":
+                continue
+            assert np.array_equal(got.cpu().numpy(), getattr(st, name)), (t, name)
+        assert int(layer.cache.n_miss.item()) == 0
+        assert np.array_equal(layer.cache.slot_expert.cpu().numpy(), se0)
+        err = ogemm.rel_err(out.float().cpu().numpy(), oracle_layer(x, ids, tw, pool))
+        assert err <= TOL, f"step {t}: rel err {err:.3e}"
+    assert cold_rows > 0, "the trace must route experts outside the resident set"
