@@ -12,7 +12,9 @@ with routed weights, moe_sum -- captured once as a HIP graph and replayed with n
 
 `value` is ms per 52-layer step with every input resident in HBM: the miss gather, which reads
 pinned host memory over PCIe, is timed in a second graph and reported as
-`e2e_with_gather_ms_per_step`; the same step at B=1 (5 tokens) is `b1_ms_per_step`. The
+`e2e_with_gather_ms_per_step` (the gather overlapped with the GEMMs of the rows already
+resident; `e2e_no_overlap_ms_per_step` is the same steps with the gather in front of every
+GEMM); the same step at B=1 (5 tokens) is `b1_ms_per_step`. The
 static hot/cold arm (inserts disabled: the warm-start set stays resident and every other
 routed expert is read over PCIe by the GEMMs, every step) is `e2e_static_arm_ms_per_step`.
 
@@ -107,10 +109,11 @@ def build(torch, pkg, rows, steps, dev, pool_dev, host_full, layers_cache=None,
     return layers, ids
 
 
-def capture(torch, layers, ids_static, tw, hbuf, gather, side):
+def capture(torch, layers, ids_static, tw, hbuf, gather, side, overlap=None):
     def step():
         for l, layer in enumerate(layers):
-            layer.apply(hbuf[l + 1], hbuf[l], tw, ids_static[l], gather=gather, side=side)
+            layer.apply(hbuf[l + 1], hbuf[l], tw, ids_static[l], gather=gather, side=side,
+                        overlap=overlap)
     # one eager step first (loads every kernel), then the cache state is put back
     snap = snapshot(torch, layers)
     step()
@@ -586,6 +589,11 @@ def main():
            "roofline": roof, "lru_fused_us_per_layer": round(lru_us, 2),
            "wall_s_timed": round(wall4, 3)}
     if not args.only_b4:
+        # the gather overlapped with the resident rows' GEMMs (the default), then the same
+        # steps from the same cache state with the gather in front of every GEMM
+        del gB
+        snap = snapshot(torch, layers4)
+        t_e2e = t
         gA = capture(torch, layers4, ids4_static, tw4, hb4, gather=True, side=side)
         run_steps(torch, gA, ids4_dev, ids4_static, t, 1)
         t += 1
@@ -596,7 +604,16 @@ def main():
         nm = [int(L.cache.n_miss.item()) for L in layers4]
         out["misses_per_layer_last_step"] = round(float(np.mean(nm)), 2)
         log(f"B=4 with PCIe miss gather: {mse:.3f} ms")
-        del gA, gB
+        del gA
+        torch.cuda.synchronize()
+        restore(layers4, snap)
+        gN = capture(torch, layers4, ids4_static, tw4, hb4, gather=True, side=side,
+                     overlap=False)
+        run_steps(torch, gN, ids4_dev, ids4_static, t_e2e, 1)
+        msn, _ = time_steps(torch, gN, ids4_dev, ids4_static, t_e2e + 1, args.steps)
+        out["e2e_no_overlap_ms_per_step"] = round(msn, 3)
+        log(f"B=4 with PCIe miss gather, not overlapped: {msn:.3f} ms")
+        del gN, snap
         torch.cuda.synchronize()
         # A/B control: the static hot/cold arm (inserts disabled: the warm-start set stays
         # resident, every other routed expert is read over PCIe by the GEMMs, every step)

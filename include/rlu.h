@@ -71,6 +71,17 @@ int r4d_lru_gather(void* d0, const void* s0, long b0, void* d1, const void* s1, 
                    const int* miss, const int* n_miss, int chunks, int lanes,
                    hipStream_t stream);
 
+/* The bucket split of the three-way gather overlap (docs/REVIEW.md:281-301 proposes it; the
+ * reference has no kernel for it). From the hot align's eids_hot[nb] (slot per block, -1 =
+ * skip) and this step's miss list (miss[cap][2] = (expert, slot), n_miss[0] entries): eids_res
+ * keeps the blocks whose slot was resident before the manager ran, eids_new the blocks whose
+ * slot the manager installed; the other entry of each pair is -1. A grouped GEMM over eids_res
+ * (and the cold align) may run while r4d_lru_gather copies; one over eids_new runs after it.
+ * Together they write the rows one GEMM over eids_hot writes, bit for bit.
+ * Limits: nb >= 0, miss_cap >= 0, 1 <= S <= 1024; -1 outside them. */
+int rlu_lru_split_fresh(const int* eids_hot, int nb, const int* miss, const int* n_miss,
+                        int miss_cap, int S, int* eids_res, int* eids_new, hipStream_t stream);
+
 /* ---- activation quant, SiLU-mul-quant, top-k reduction ----------------------------------
  * bf16 activations (uint16 bit patterns), e4m3fn outputs (one byte each), float32 scales.
  * group = 128: one scale per 128 columns (per-token-group-128, the GEMM input format of this

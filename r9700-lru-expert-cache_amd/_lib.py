@@ -23,6 +23,7 @@ SIGNATURES: dict[str, tuple] = {
     "r4d_lru_manage": (_I, [_P] + [_I] * 5 + [_P] * 9),
     "r4d_lru_fused": (_I, [_P] + [_I] * 5 + [_P] * 8 + [_I] * 3 + [_P] * 7),
     "r4d_lru_gather": (_I, [_P, _P, _L] * 6 + [_P, _P, _I, _I, _P]),
+    "rlu_lru_split_fresh": (_I, [_P, _I, _P, _P, _I, _I, _P, _P, _P]),
     "rlu_lru_fused_quant": (_I, [_P] + [_I] * 5 + [_P] * 8 + [_I] * 3 + [_P] * 7 + [_I] * 3
                             + [_P] * 3),
     "rlu_quant_fp8_group": (_I, [_P, _I, _I, _I, _I, _P, _P, _P]),

@@ -763,6 +763,34 @@ __global__ __launch_bounds__(NT) void gather_k(v4u* d0, const v4u* s0, long v0,
   }
 }
 
+// Splits the hot align's block expert ids (slot indices) by whether this step's gather
+// writes the slot: eids_res keeps the slots resident before the manager ran (-1 elsewhere),
+// eids_new keeps the slots the manager just installed (the miss list's slot column). A GEMM
+// over eids_res needs no gathered byte, so it can run while the gather copies; one over
+// eids_new runs after it. Every block lands in exactly one of the two (or neither, for -1).
+// One workgroup: a slot bitmap in LDS, then one pass over the blocks.
+__global__ __launch_bounds__(NT) void split_fresh_k(const int* __restrict__ eids, int nb,
+                                                    const int* __restrict__ miss,
+                                                    const int* __restrict__ n_miss, int cap,
+                                                    int S, int* __restrict__ eids_res,
+                                                    int* __restrict__ eids_new) {
+  __shared__ unsigned char fresh[MAXS];
+  for (int s = threadIdx.x; s < S; s += NT) fresh[s] = 0;
+  __syncthreads();
+  const int nm = min(n_miss[0], cap);
+  for (int j = threadIdx.x; j < nm; j += NT) {
+    const int sl = miss[2 * j + 1];
+    if ((unsigned)sl < (unsigned)S) fresh[sl] = 1;
+  }
+  __syncthreads();
+  for (int b = threadIdx.x; b < nb; b += NT) {
+    const int s = eids[b];
+    const bool f = (unsigned)s < (unsigned)S && fresh[s];
+    eids_res[b] = f ? -1 : s;
+    eids_new[b] = f ? s : -1;
+  }
+}
+
 }  // namespace rlu
 
 extern "C" {
@@ -840,6 +868,18 @@ int r4d_lru_gather(void* d0, const void* s0, long b0, void* d1, const void* s1, 
                      (rlu::v4u*)d3, (const rlu::v4u*)s3, b3 / 16, (rlu::v4u*)d4,
                      (const rlu::v4u*)s4, b4 / 16, (rlu::v4u*)d5, (const rlu::v4u*)s5, b5 / 16,
                      miss, n_miss);
+  return (int)hipGetLastError();
+}
+
+// The bucket split of the three-way overlap proposed in docs/REVIEW.md:281-301 (no kernel in
+// the reference).
+int rlu_lru_split_fresh(const int* eids_hot, int nb, const int* miss, const int* n_miss,
+                        int miss_cap, int S, int* eids_res, int* eids_new,
+                        hipStream_t stream) {
+  if (nb < 0 || miss_cap < 0 || S <= 0 || S > rlu::MAXS) return -1;
+  if (nb == 0) return 0;
+  hipLaunchKernelGGL(rlu::split_fresh_k, dim3(1), dim3(rlu::NT), 0, stream, eids_hot, nb, miss,
+                     n_miss, miss_cap, S, eids_res, eids_new);
   return (int)hipGetLastError();
 }
 

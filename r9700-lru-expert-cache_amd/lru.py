@@ -19,11 +19,15 @@ from ._lib import check, lib, stream_ptr
 
 _P = ctypes.c_void_p
 
-# reference defaults (r4d_mxfp4_moe.py.lru.diff:144-151)
+# the reference's knobs and defaults (r4d_mxfp4_moe.py.lru.diff:144-151), except the gather
+# geometry: the reference's 8 chunks x 16 lanes keeps ~2 MB of host reads in flight on
+# MI355X, which the link does not need (it saturates at ~58 GB/s with far less) and which
+# slows every kernel running beside the gather several-fold. 4 x 32 was the fastest
+# measured for a 52-layer decode step with the gather overlapped (20 rows, ~9 misses/layer).
 LRU_THRESH = float(os.environ.get("VLLM_R4D_LRU_THRESH", "0.5"))
 LRU_MAX_INSERTS = int(os.environ.get("VLLM_R4D_LRU_MAX_INSERTS", "64"))
-LRU_CHUNKS = int(os.environ.get("VLLM_R4D_LRU_CHUNKS", "8"))
-LRU_LANES = int(os.environ.get("VLLM_R4D_LRU_LANES", "16"))
+LRU_CHUNKS = int(os.environ.get("VLLM_R4D_LRU_CHUNKS", "4"))
+LRU_LANES = int(os.environ.get("VLLM_R4D_LRU_LANES", "32"))
 BLOCK = 16
 
 
@@ -87,6 +91,22 @@ def _r4d_lru_gather(dsts: list[torch.Tensor], srcs: list[torch.Tensor], miss: to
     rc = lib().r4d_lru_gather(*args, _ptr(miss), _ptr(n_miss), chunks, lanes,
                               _P(stream_ptr()))
     check(rc, "r4d_lru_gather (slab sizes must be 16B multiples)")
+
+
+def split_fresh(eids_hot: torch.Tensor, miss: torch.Tensor, n_miss: torch.Tensor, S: int,
+                eids_res: torch.Tensor, eids_new: torch.Tensor) -> None:
+    """The bucket split of the three-way gather overlap (docs/REVIEW.md:281-301): eids_res
+    <- the blocks of eids_hot whose slot was resident before this step's manager ran,
+    eids_new <- the blocks whose slot it installed (the slot column of miss[:n_miss]); -1 in
+    the other. Each is a valid expert-id array for the grouped GEMM's row contract."""
+    for t in (eids_hot, miss, n_miss, eids_res, eids_new):
+        assert t.dtype == torch.int32 and t.is_contiguous()
+    nb = eids_hot.numel()
+    assert eids_res.numel() == nb and eids_new.numel() == nb and miss.shape[-1] == 2
+    rc = lib().rlu_lru_split_fresh(_ptr(eids_hot), nb, _ptr(miss), _ptr(n_miss),
+                                   miss.numel() // 2, S, _ptr(eids_res), _ptr(eids_new),
+                                   _P(stream_ptr()))
+    check(rc, "rlu_lru_split_fresh")
 
 
 def _r4d_lru_fused(topk_ids: torch.Tensor, table: torch.Tensor, map_cold: torch.Tensor,

@@ -6,7 +6,8 @@ r4d_mxfp4_moe.py.lru.diff): _build_hot / _build_lru (:453-541) -> LruMoELayer.__
 _lru_step_fused (:557-579) -> _lru_step_fused, _gemm_split (:584-607) -> _gemm_split,
 _act_quant (:640-657) -> _act_quant, _apply_split (:659-696) -> apply. The experts are fp8 e4m3
 with 128x128 float32 block scales (w13 [E, 2I, H], w2 [E, H, I]); the activation quant is
-per-token-group-128. The miss gather runs on a side stream and the GEMMs wait for it.
+per-token-group-128. The miss gather runs on a side stream; the GEMMs over rows it does not
+write run beside it, the others wait for it (apply's overlap).
 
 Every buffer a step touches is allocated here, once, for a fixed token count, so a step can be
 captured into a HIP graph and replayed with new routing (only contents change).
@@ -20,7 +21,7 @@ import torch
 
 from . import ops
 from ._lib import check, lib, stream_ptr
-from .lru import LRU_CHUNKS, LRU_LANES, LruCache, _r4d_lru_gather
+from .lru import LRU_CHUNKS, LRU_LANES, LruCache, _r4d_lru_gather, split_fresh
 
 _P = ctypes.c_void_p
 BLOCK = 16
@@ -95,6 +96,9 @@ class LruMoELayer:
                       LruCache.build(self.E, hot, rank, dev, max_inserts=max_inserts))
         # align outputs and intermediates for exactly max_tokens rows
         self.align = self.cache.alloc_align(self.mtk, BLOCK)
+        self.eids_res = torch.empty_like(self.align[1])
+        self.eids_new = torch.empty_like(self.align[1])
+        self.ev_up = torch.cuda.Event()
         self.qx = torch.empty((self.M, self.H), dtype=ops.FP8, device=dev)
         self.xs = torch.empty((self.M, self.H // 128), dtype=torch.float32, device=dev)
         self.ic1 = torch.empty((self.mtk, self.N1), dtype=torch.bfloat16, device=dev)
@@ -120,9 +124,13 @@ class LruMoELayer:
 
     # -- _lru_step_fused: manager + both aligns in one launch, then the miss gather -----------
     def _lru_step_fused(self, topk_ids: torch.Tensor, gather: bool, side: torch.cuda.Stream | None,
-                        hidden_states: torch.Tensor | None = None):
+                        hidden_states: torch.Tensor | None = None, split: bool = False):
         """The fused manager + align; with hidden_states, the same launch also quantizes them
-        into (qx, xs) (the cache and the quant are independent and both feed GEMM1)."""
+        into (qx, xs) (the cache and the quant are independent and both feed GEMM1).
+
+        split (with a side stream): the gather runs as two launches, the gate_up buffers
+        (w13, s13) first and then the down buffers (w2, s2), with self.ev_up recorded between
+        them, so that gate_up over the installed slots can start while w2 is still arriving."""
         if hidden_states is None:
             self.cache.fused(topk_ids, out=self.align, block_size=BLOCK)
         else:
@@ -130,29 +138,40 @@ class LruMoELayer:
                                    block_size=BLOCK)
         if not gather:
             return None
-        # six-buffer ABI of the reference gather: the fp8 format has four per-expert buffers,
-        # the two spare pairs repeat the (small) scale buffers
-        dsts = [self.slots.w13, self.slots.w2, self.slots.s13, self.slots.s2,
-                self.slots.s13, self.slots.s2]
-        srcs = [self.full.w13, self.full.w2, self.full.s13, self.full.s2,
-                self.full.s13, self.full.s2]
-        sp = [self.full_ptrs[0], self.full_ptrs[2], self.full_ptrs[1], self.full_ptrs[3],
-              self.full_ptrs[1], self.full_ptrs[3]]
+        w13, s13, w2, s2 = ((self.slots.w13, self.full.w13, self.full_ptrs[0]),
+                            (self.slots.s13, self.full.s13, self.full_ptrs[1]),
+                            (self.slots.w2, self.full.w2, self.full_ptrs[2]),
+                            (self.slots.s2, self.full.s2, self.full_ptrs[3]))
+        # six-buffer ABI of the reference gather: the fp8 format has four per-expert buffers;
+        # spare pairs repeat a (small) scale buffer -- the same bytes to the same place
+        if split and side is not None:
+            parts = [[w13, s13, s13, s13, s13, s13], [w2, s2, s2, s2, s2, s2]]
+        else:
+            parts = [[w13, w2, s13, s2, s13, s2]]
         cur = torch.cuda.current_stream()
         if side is None:
-            _r4d_lru_gather(dsts, srcs, self.cache.miss, self.cache.n_miss, LRU_CHUNKS,
-                            LRU_LANES, src_ptrs=sp)
+            for p in parts:
+                self._gather(p)
             return None
         side.wait_stream(cur)
         with torch.cuda.stream(side):
-            _r4d_lru_gather(dsts, srcs, self.cache.miss, self.cache.n_miss, LRU_CHUNKS,
-                            LRU_LANES, src_ptrs=sp)
+            for i, p in enumerate(parts):
+                self._gather(p)
+                if i + 1 < len(parts):
+                    self.ev_up.record(side)
         return side
+
+    def _gather(self, pairs):
+        _r4d_lru_gather([d for d, _, _ in pairs], [s for _, s, _ in pairs], self.cache.miss,
+                        self.cache.n_miss, LRU_CHUNKS, LRU_LANES,
+                        src_ptrs=[p for _, _, p in pairs])
 
     # -- _gemm_split: resident slots + the full tensor, one launch ----------------------------
     def _gemm_split(self, y, qx, xs, slot_w, slot_s, full_w_ptr, full_s_ptr, tw, top_k, npw,
-                    sk):
-        sh, eh, nh, sc, ec, nc = self.align
+                    sk, eh=None):
+        """eh replaces the hot align's block expert ids (the overlap's resident bucket)."""
+        sh, eh0, nh, sc, ec, nc = self.align
+        eh = eh0 if eh is None else eh
         K = qx.shape[1]
         N = slot_w.shape[1]
         rc = lib().rlu_moe_gemm_split(
@@ -163,28 +182,61 @@ class LruMoELayer:
             y.shape[0], top_k, K, N, self.wv, sk, npw, _P(stream_ptr()))
         check(rc, "rlu_moe_gemm_split")
 
+    # -- the hot GEMM alone over a bucket of slots (the overlap's installed bucket) -----------
+    def _gemm_hot(self, y, qx, xs, slot_w, slot_s, tw, top_k, npw, sk, eh):
+        sh, _, nh = self.align[:3]
+        ops._r4d_fp8_moe_gemm_into(y, qx, xs, slot_w, slot_s, None, sh, eh, nh, tw, y.shape[0],
+                                   top_k, self.wv, sk, npw)
+
     # -- _act_quant: fused silu-and-mul + group-128 quant --------------------------------------
     def _act_quant(self):
         ops.silu_mul_quant(self.ic1, group=ops.GROUP, out=(self.q2, self.s2))
 
     def apply(self, output: torch.Tensor, hidden_states: torch.Tensor, topk_weights: torch.Tensor,
               topk_ids: torch.Tensor, gather: bool = True,
-              side: torch.cuda.Stream | None = None) -> None:
+              side: torch.cuda.Stream | None = None, overlap: bool | None = None) -> None:
         """_apply_split: output [M, H] bf16 <- hidden_states [M, H] bf16 routed by topk_ids /
-        topk_weights [M, top_k]."""
+        topk_weights [M, top_k].
+
+        overlap (needs gather and a side stream; default on when the cache can insert): the
+        three-way split of docs/REVIEW.md:281-301. While the side stream gathers this step's
+        installs, the main stream runs gate_up, SiLU-quant and down over the rows of slots
+        resident before the manager ran plus the cold rows. Then gate_up and SiLU-quant over
+        the rows of the installed slots, once their w13 has arrived (the gather copies w13
+        and s13 first, w2 and s2 second), down over them once all of it has, and moe_sum.
+        Every row is computed by the same kernel with the same split as without the overlap,
+        so the output is bit-identical."""
         M = hidden_states.shape[0]
         assert M == self.M and topk_ids.shape == (M, self.top_k)
-        waited = self._lru_step_fused(topk_ids, gather, side, hidden_states)
-        if waited is not None:
-            torch.cuda.current_stream().wait_stream(waited)
-        self._gemm_split(self.ic1, self.qx, self.xs, self.slots.w13, self.slots.s13,
-                         self.full_ptrs[0], self.full_ptrs[1], None, self.top_k, self.npw1,
-                         self.sk1)
-        self._act_quant()
+        if overlap is None:
+            overlap = self.cache.max_inserts > 0
+        overlap = overlap and gather and side is not None
+        waited = self._lru_step_fused(topk_ids, gather, side, hidden_states, split=overlap)
         tw = topk_weights.reshape(-1)
         if tw.dtype != torch.float32 or not tw.is_contiguous():   # as fused_topk already gives
             self.tw.copy_(tw)
             tw = self.tw
-        self._gemm_split(self.ic3, self.q2, self.s2, self.slots.w2, self.slots.s2,
-                         self.full_ptrs[2], self.full_ptrs[3], tw, 1, self.npw2, self.sk2)
+        up = (self.ic1, self.qx, self.xs, self.slots.w13, self.slots.s13)
+        down = (self.ic3, self.q2, self.s2, self.slots.w2, self.slots.s2)
+        if overlap:
+            split_fresh(self.align[1], self.cache.miss, self.cache.n_miss, self.cache.S,
+                        self.eids_res, self.eids_new)
+            self._gemm_split(*up, self.full_ptrs[0], self.full_ptrs[1], None, self.top_k,
+                             self.npw1, self.sk1, eh=self.eids_res)
+            self._act_quant()
+            self._gemm_split(*down, self.full_ptrs[2], self.full_ptrs[3], tw, 1, self.npw2,
+                             self.sk2, eh=self.eids_res)
+            torch.cuda.current_stream().wait_event(self.ev_up)
+            self._gemm_hot(*up, None, self.top_k, self.npw1, self.sk1, self.eids_new)
+            self._act_quant()
+            torch.cuda.current_stream().wait_stream(waited)
+            self._gemm_hot(*down, tw, 1, self.npw2, self.sk2, self.eids_new)
+        else:
+            if waited is not None:
+                torch.cuda.current_stream().wait_stream(waited)
+            self._gemm_split(*up, self.full_ptrs[0], self.full_ptrs[1], None, self.top_k,
+                             self.npw1, self.sk1)
+            self._act_quant()
+            self._gemm_split(*down, self.full_ptrs[2], self.full_ptrs[3], tw, 1, self.npw2,
+                             self.sk2)
         ops.moe_sum(self.ic3.view(M, self.top_k, self.H), output)

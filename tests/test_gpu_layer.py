@@ -153,3 +153,41 @@ def test_layer_static_arm(pkg, pool):
         err = ogemm.rel_err(out.float().cpu().numpy(), oracle_layer(x, ids, tw, pool))
         assert err <= TOL, f"step {t}: rel err {err:.3e}"
     assert cold_rows > 0, "the trace must route experts outside the resident set"
+
+
+@pytest.mark.parametrize("M", [5, 20])
+def test_layer_overlap_bit_identical(pkg, pool, M):
+    """The three-way split (docs/REVIEW.md:281-301): resident and cold rows computed while the
+    side stream gathers, installed rows after it. Two layers from the same warm start, one
+    with the overlap and one without, see the same steps: outputs equal bit for bit, cache
+    states equal, and the output stays within 2e-2 of the oracle pipeline."""
+    steps = 4
+    tr, perm0 = trace.zipf_trace(seed=400 + M, E=E, rows=M, k=TOPK, steps=steps, s=1.1,
+                                 corr=0.7 if M >= 20 else 0.0)
+    ids_all = tr.reshape(steps, M, TOPK).astype(np.int32)
+    hot, rank = trace.warm_hot(perm0, S)
+    full = pkg.ExpertWeights(pool["w13"], pool["w13s"], pool["w2"], pool["w2s"])
+    a = pkg.LruMoELayer(full, hot, rank, M, TOPK, DEV)
+    b = pkg.LruMoELayer(full, hot, rank, M, TOPK, DEV)
+    rng = np.random.default_rng(400 + M)
+    side = torch.cuda.Stream()
+    installs = 0
+    for t in range(steps):
+        ids = ids_all[t]
+        x = fp8.bf16_round(rng.standard_normal((M, H)).astype(np.float32))
+        tw = rng.random((M, TOPK)).astype(np.float32)
+        xd = torch.from_numpy(x).to(torch.bfloat16).to(DEV)
+        twd, idd = torch.from_numpy(tw).to(DEV), torch.from_numpy(ids).to(DEV)
+        oa = torch.empty((M, H), dtype=torch.bfloat16, device=DEV)
+        ob = torch.empty((M, H), dtype=torch.bfloat16, device=DEV)
+        gpu_case(f"overlap layer M={M} step {t}")
+        a.apply(oa, xd, twd, idd, gather=True, side=side, overlap=True)
+        b.apply(ob, xd, twd, idd, gather=True, side=side, overlap=False)
+        torch.cuda.synchronize()
+        installs += int(a.cache.n_miss.item())
+        assert torch.equal(oa.view(torch.int16), ob.view(torch.int16)), f"step {t}"
+        for name, ga, gb in zip(olru.LruState.NAMES, a.cache.state(), b.cache.state()):
+            assert torch.equal(ga, gb), (t, name)
+        err = ogemm.rel_err(oa.float().cpu().numpy(), oracle_layer(x, ids, tw, pool))
+        assert err <= TOL, f"step {t}: rel err {err:.3e}"
+    assert installs > 0, "the trace must install experts"

@@ -375,3 +375,67 @@ def test_fused_quant_equals_fused_then_quant(pkg, rows):
             assert torch.equal(ta, tb)
         assert torch.equal(q1.view(torch.uint8), q2.view(torch.uint8))
         assert torch.equal(s1, s2)
+
+
+@pytest.mark.parametrize("rows,seed", [(5, 1), (20, 2), (20, 3)])
+def test_split_fresh_partitions_the_hot_align(pkg, rows, seed):
+    """rlu_lru_split_fresh on the fused kernel's own outputs, over steps of a Zipf trace: each
+    block of eids_hot lands in exactly one bucket (-1 blocks in neither); a block is in the
+    installed bucket exactly when its slot changed hands this step (slot_expert before the
+    step differs), i.e. when the gather writes it."""
+    from importlib import import_module
+    lru = import_module(pkg.__name__ + ".lru")
+    E, S, steps = 128, 100, 4
+    tr, perm0 = pkg.traces.zipf_trace(seed=seed, E=E, rows=rows, k=10, steps=steps, s=1.1,
+                                      corr=0.7 if rows >= 20 else 0.0)
+    hot, rank = pkg.traces.warm_hot(perm0, S)
+    cache = lru.LruCache.build(E, hot, rank, DEV, thresh=1.0)
+    out = cache.alloc_align(rows * 10, BS)
+    res, new = torch.empty_like(out[1]), torch.empty_like(out[1])
+    seen_new = 0
+    for t in range(steps):
+        gpu_case(f"split_fresh rows={rows} seed={seed} step {t}")
+        before = cache.slot_expert.cpu().numpy().copy()
+        cache.fused(torch.from_numpy(tr[t]).to(DEV), out=out, block_size=BS)
+        lru.split_fresh(out[1], cache.miss, cache.n_miss, S, res, new)
+        torch.cuda.synchronize()
+        eids = out[1].cpu().numpy()
+        r, n = res.cpu().numpy(), new.cpu().numpy()
+        after = cache.slot_expert.cpu().numpy()
+        live = eids >= 0
+        assert (r[~live] == -1).all() and (n[~live] == -1).all()
+        changed = np.zeros(S, bool)
+        changed[before != after] = True
+        for b in np.nonzero(live)[0]:
+            s = eids[b]
+            if changed[s]:
+                assert n[b] == s and r[b] == -1, (t, b)
+                seen_new += 1
+            else:
+                assert r[b] == s and n[b] == -1, (t, b)
+    assert seen_new > 0, "the trace must install experts"
+
+
+def test_split_fresh_clamps_to_the_miss_capacity(pkg):
+    """n_miss larger than the miss buffer reads only the buffer; bad sizes return -1."""
+    from importlib import import_module
+    lru = import_module(pkg.__name__ + ".lru")
+    lib = pkg._lib.lib()
+    eids = torch.tensor([3, 5, 7, 3, -1, -1], dtype=torch.int32, device=DEV)
+    miss = torch.tensor([[9, 5], [11, 7]], dtype=torch.int32, device=DEV)
+    n_miss = torch.tensor([7], dtype=torch.int32, device=DEV)
+    res, new = torch.empty_like(eids), torch.empty_like(eids)
+    gpu_case("split_fresh clamp")
+    lru.split_fresh(eids, miss, n_miss, 8, res, new)
+    torch.cuda.synchronize()
+    assert res.tolist() == [3, -1, -1, 3, -1, -1]
+    assert new.tolist() == [-1, 5, 7, -1, -1, -1]
+    n_miss.fill_(0)
+    lru.split_fresh(eids, miss, n_miss, 8, res, new)
+    torch.cuda.synchronize()
+    assert res.tolist() == eids.tolist() and new.tolist() == [-1] * 6
+    P = ctypes.c_void_p
+    for nb, cap, S in ((-1, 2, 8), (6, -1, 8), (6, 2, 0), (6, 2, 1025)):
+        assert lib.rlu_lru_split_fresh(P(eids.data_ptr()), nb, P(miss.data_ptr()),
+                                       P(n_miss.data_ptr()), cap, S, P(res.data_ptr()),
+                                       P(new.data_ptr()), None) == -1
