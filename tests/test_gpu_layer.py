@@ -191,3 +191,57 @@ def test_layer_overlap_bit_identical(pkg, pool, M):
         err = ogemm.rel_err(oa.float().cpu().numpy(), oracle_layer(x, ids, tw, pool))
         assert err <= TOL, f"step {t}: rel err {err:.3e}"
     assert installs > 0, "the trace must install experts"
+
+
+def test_layer_overlap_graph_replay(pkg, pool):
+    """The overlapped step captured once as a HIP graph (side-stream gather, event between its
+    two launches, joins) and replayed with new routing: every replay's output and cache state
+    equal an eager layer without the overlap, bit for bit, with eager work and
+    synchronizations between the replays."""
+    M, steps = 20, 5
+    tr, perm0 = trace.zipf_trace(seed=77, E=E, rows=M, k=TOPK, steps=steps, s=1.1, corr=0.7)
+    ids_all = tr.reshape(steps, M, TOPK).astype(np.int32)
+    hot, rank = trace.warm_hot(perm0, S)
+    full = pkg.ExpertWeights(pool["w13"], pool["w13s"], pool["w2"], pool["w2s"])
+    a = pkg.LruMoELayer(full, hot, rank, M, TOPK, DEV)
+    b = pkg.LruMoELayer(full, hot, rank, M, TOPK, DEV)
+    rng = np.random.default_rng(77)
+    xs = [torch.from_numpy(fp8.bf16_round(rng.standard_normal((M, H)).astype(np.float32)))
+          .to(torch.bfloat16).to(DEV) for _ in range(steps)]
+    tws = [torch.from_numpy(rng.random((M, TOPK)).astype(np.float32)).to(DEV)
+           for _ in range(steps)]
+    x_st, tw_st = torch.empty_like(xs[0]), torch.empty_like(tws[0])
+    ids_st = torch.empty((M, TOPK), dtype=torch.int32, device=DEV)
+    out_a = torch.empty((M, H), dtype=torch.bfloat16, device=DEV)
+    out_b = torch.empty_like(out_a)
+    side = torch.cuda.Stream()
+    # step 0 eager on both (loads every kernel), then capture the overlapped step
+    gpu_case("overlap graph: eager step 0")
+    ids0 = torch.from_numpy(ids_all[0]).to(DEV)
+    a.apply(out_a, xs[0], tws[0], ids0, gather=True, side=side, overlap=True)
+    b.apply(out_b, xs[0], tws[0], ids0, gather=True, side=side, overlap=False)
+    torch.cuda.synchronize()
+    assert torch.equal(out_a.view(torch.int16), out_b.view(torch.int16))
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        a.apply(out_a, x_st, tw_st, ids_st, gather=True, side=side, overlap=True)
+    torch.cuda.synchronize()
+    installs = 0
+    for t in range(1, steps):
+        gpu_case(f"overlap graph: replay step {t}")
+        ids = torch.from_numpy(ids_all[t]).to(DEV)
+        x_st.copy_(xs[t])
+        tw_st.copy_(tws[t])
+        ids_st.copy_(ids)
+        g.replay()
+        b.apply(out_b, xs[t], tws[t], ids, gather=True, side=side, overlap=False)
+        torch.cuda.synchronize()
+        installs += int(a.cache.n_miss.item())
+        assert torch.equal(out_a.view(torch.int16), out_b.view(torch.int16)), f"replay {t}"
+        for name, ga, gb in zip(olru.LruState.NAMES, a.cache.state(), b.cache.state()):
+            assert torch.equal(ga, gb), (t, name)
+        assert torch.equal(a.slots.w2.view(torch.uint8), b.slots.w2.view(torch.uint8)), t
+        out_a.zero_()                       # eager work between replays
+        torch.cuda.synchronize()
+    assert installs > 0, "the trace must install experts"
+    del g
