@@ -306,6 +306,10 @@ def lm_head_w4(torch, pkg, dev, Ms=(1, 4, 8), reps=20):
         x = torch.randn(M, K, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16).to(dev)
         y = torch.empty((M, P[0].n_pad), dtype=torch.bfloat16, device=dev)
         nbytes = P[0].nbytes + M * K * 2 + M * N * 2
+        # every M starts from the same power state: back to back, this kernel slows by up to
+        # a fifth after a few ms (its dequant work draws enough power to lower the clocks)
+        torch.cuda.synchronize()
+        time.sleep(0.25)
         for i in range(2):
             w4.gemm_w4a16(x, P[i], out=y)
         torch.cuda.synchronize()

@@ -10,17 +10,19 @@
 //   sz      [N/16][K/128][16] u32: bf16 scale bits in the low half, the integer zero (int16,
 //           |zero| <= 1024) in the high half; row within the tile is the last axis.
 //
-// Dequant is two VALU ops per bf16 pair: ((D >> 4t) & 0x000F000F) | 0x43004300 is the bf16
-// pair (128 + q_2t, 128 + q_2t+1), exact. The MFMA then gives d = sum_k x_k (128 + q_k) per
-// group, and the group's contribution is scale * (d - (128 + zero) * sum_k x_k): the offset and
-// the zero come back out through the per-(row, group) activation sum, computed once per
-// workgroup. Activations stay bf16 (the reference widened bf16 to f16 for its gfx1201 WMMA).
+// Dequant: ((D >> 4t) & 0x000F000F) | 0x43004300 is the bf16 pair (128 + q_2t, 128 + q_2t+1),
+// exact; one v_and_or_b32 per pair, the shifts done 64 bits (two dwords) at a time. The MFMA
+// then gives d = sum_k x_k (128 + q_k) per group, and the group's contribution is
+// scale * (d - (128 + zero) * sum_k x_k). Per tile only scale * d is accumulated; the offset and
+// zero terms of all of a wave's groups come out once per item through an f32 MFMA of the
+// per-(row, group) activation sums (computed once per workgroup) against scale * (128 + zero).
+// Activations stay bf16 (the reference widened bf16 to f16 for its gfx1201 WMMA).
 //
 // Work split: an item is SS 16-row strips (16 SS columns). SKW waves split K; a workgroup of 8
 // waves runs 8 / SKW items at once. x (<= 16 rows, zero-padded) is staged once per workgroup in
 // LDS in A-operand fragment order, so each A read is a conflict-free 1 KB ds_read_b128 shared by
 // the SS strips of a group; each wave computes the per-(row, group) sums of x for its groups with
-// an MFMA against a B of ones. Per group a wave dequantizes its SS 1 KB tiles and runs SS
+// an MFMA of ones. Per group a wave dequantizes its SS 1 KB tiles and runs SS
 // independent MFMA chains. Its register ring is one item deep: after consuming a tile it issues
 // the same tile of its next item, so a whole item (SS x G / SKW KB per wave) is in flight behind
 // the one being computed. The K splits' partial sums are added in LDS in a fixed order
@@ -42,6 +44,8 @@ constexpr int WAVES = 8;
 constexpr int SS = 2;          // strips per item
 constexpr int MAXGQ = 8;       // groups per wave: K / 128 / split <= 8, so K <= 4096
 constexpr int MAXK = 4096;     // x in LDS: 16 rows x K bf16 = 2 K * 16 bytes
+constexpr int BUF_WORD3 = 0x00020000;   // raw buffer descriptor word 3 on gfx9 (no format)
+constexpr int SLC = 2;                  // buffer cache policy: streaming (the codes are read once)
 
 __device__ __forceinline__ v4f mfma_bf16(v4u a, v4u b, v4f c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a),
@@ -56,14 +60,31 @@ __device__ __forceinline__ unsigned and_or(unsigned v, unsigned mask, unsigned m
   return r;
 }
 
-// four bf16 pairs (128 + q_2t, 128 + q_2t+1) from the eight codes of one dword
-__device__ __forceinline__ v4u dequant(unsigned d, unsigned mask, unsigned magic) {
-  v4u b;
-  b.x = and_or(d, mask, magic);
-  b.y = and_or(d >> 4, mask, magic);
-  b.z = and_or(d >> 8, mask, magic);
-  b.w = and_or(d >> 12, mask, magic);
-  return b;
+// 64-bit right shift by a constant, as one instruction (the compiler splits a 64-bit shift
+// into two 32-bit ones, alignbit + shift)
+template <int S>
+__device__ __forceinline__ unsigned long long shr64(unsigned long long v) {
+  unsigned long long r;
+  asm volatile("v_lshrrev_b64 %0, %1, %2" : "=v"(r) : "i"(S), "v"(v));
+  return r;
+}
+
+// the 16 bf16 pairs (128 + q_2t, 128 + q_2t+1) of one tile lane: b[i] feeds MFMA i. One 64-bit
+// shift serves two dwords: the bits that cross into the low dword land at bit 20 and above,
+// which the mask drops.
+__device__ __forceinline__ void dequant(v4u w, unsigned mask, unsigned magic, v4u* b) {
+  const unsigned long long p0 = ((unsigned long long)w.y << 32) | w.x;
+  const unsigned long long p1 = ((unsigned long long)w.w << 32) | w.z;
+  const unsigned long long a4 = shr64<4>(p0), a8 = shr64<8>(p0), a12 = shr64<12>(p0);
+  const unsigned long long c4 = shr64<4>(p1), c8 = shr64<8>(p1), c12 = shr64<12>(p1);
+  b[0] = v4u{and_or(w.x, mask, magic), and_or((unsigned)a4, mask, magic),
+             and_or((unsigned)a8, mask, magic), and_or((unsigned)a12, mask, magic)};
+  b[1] = v4u{and_or(w.y, mask, magic), and_or((unsigned)(a4 >> 32), mask, magic),
+             and_or((unsigned)(a8 >> 32), mask, magic), and_or((unsigned)(a12 >> 32), mask, magic)};
+  b[2] = v4u{and_or(w.z, mask, magic), and_or((unsigned)c4, mask, magic),
+             and_or((unsigned)c8, mask, magic), and_or((unsigned)c12, mask, magic)};
+  b[3] = v4u{and_or(w.w, mask, magic), and_or((unsigned)(c4 >> 32), mask, magic),
+             and_or((unsigned)(c8 >> 32), mask, magic), and_or((unsigned)(c12 >> 32), mask, magic)};
 }
 
 template <int SKW, int GQ>
@@ -95,15 +116,29 @@ __global__ __launch_bounds__(WAVES * WAVE) void gemv_k(const uint16_t* __restric
     xa[u] = v;
   }
   __syncthreads();
-  // per-(row, group) sums of x in the D layout (rows 4 c4 + i): an MFMA against ones
-  v4f xsum[GQ];
-  const v4u ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
+  // per-(row, group) sums of x as the A operand of the zero-correction MFMA (f32 16x16x4):
+  // lane (c4, r16) holds minus the sum of row r16 over group g0 + c4 + 4 j (0 past GQ). The
+  // x fragments in A order, read as a B operand, are x transposed, so an MFMA of ones against
+  // them leaves row r16's sum in every register of lane (c4, r16).
+  constexpr int NJ = (GQ + 3) / 4;
+  float xs_a[NJ];
+  {
+    const v4u ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
+    float s[GQ];
 #pragma unroll
-  for (int g = 0; g < GQ; ++g) {
-    v4f d = {0.f, 0.f, 0.f, 0.f};
+    for (int g = 0; g < GQ; ++g) {
+      v4f d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) d = mfma_bf16(xa[((g0 + g) * 4 + i) * 64 + lane], ones, d);
-    xsum[g] = d;
+      for (int i = 0; i < 4; ++i) d = mfma_bf16(ones, xa[((g0 + g) * 4 + i) * 64 + lane], d);
+      s[g] = d[0];
+    }
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      float v = 0.f;
+#pragma unroll
+      for (int g = 4 * j; g < GQ && g < 4 * j + 4; ++g) v = c4 == g - 4 * j ? s[g] : v;
+      xs_a[j] = -v;
+    }
   }
 
   const int nitems = N / (16 * SS);
@@ -111,11 +146,18 @@ __global__ __launch_bounds__(WAVES * WAVE) void gemv_k(const uint16_t* __restric
   int item = blockIdx.x * IPG + sub;
   v4u rw[U];
   unsigned rs[U];
+  // buffer loads: the tile offset is wave-uniform and rides in an SGPR (no per-load vector
+  // address arithmetic); the host keeps the byte sizes below 2^31
+  const int ntile = nitems * SS * G;
+  const __amdgpu_buffer_rsrc_t rq =
+      __builtin_amdgcn_make_buffer_rsrc((void*)wq, 0, ntile * 1024, BUF_WORD3);
+  const __amdgpu_buffer_rsrc_t rz =
+      __builtin_amdgcn_make_buffer_rsrc((void*)sz, 0, ntile * 64, BUF_WORD3);
   auto load = [&](int it, int g, int s2) {
     const int itc = it < nitems ? it : nitems - 1;  // past the end: re-read the last item
-    const size_t tile = (size_t)(itc * SS + s2) * G + g0 + g;
-    rw[g * SS + s2] = __builtin_nontemporal_load(wq + tile * 64 + lane);
-    rs[g * SS + s2] = sz[tile * 16 + r16];
+    const int tile = __builtin_amdgcn_readfirstlane((itc * SS + s2) * G + g0 + g);
+    rw[g * SS + s2] = __builtin_amdgcn_raw_buffer_load_b128(rq, lane * 16, tile * 1024, SLC);
+    rs[g * SS + s2] = __builtin_amdgcn_raw_buffer_load_b32(rz, r16 * 4, tile * 64, 0);
   };
 #pragma unroll
   for (int g = 0; g < GQ; ++g)
@@ -124,8 +166,13 @@ __global__ __launch_bounds__(WAVES * WAVE) void gemv_k(const uint16_t* __restric
   // every wave of the workgroup runs the same number of passes (the barriers below)
   for (int pass = blockIdx.x; pass * IPG < nitems; pass += gridDim.x) {
     v4f acc[SS];
+    unsigned zs[SS][NJ];            // scale/zero word of group g0 + c4 + 4 j, column r16
 #pragma unroll
-    for (int s2 = 0; s2 < SS; ++s2) acc[s2] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int s2 = 0; s2 < SS; ++s2) {
+      acc[s2] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) zs[s2][j] = 0u;
+    }
     const int next = item + stride;
 #pragma unroll
     for (int g = 0; g < GQ; ++g) {
@@ -135,18 +182,30 @@ __global__ __launch_bounds__(WAVES * WAVE) void gemv_k(const uint16_t* __restric
 #pragma unroll
       for (int s2 = 0; s2 < SS; ++s2) {
         const int j = g * SS + s2;
-        const v4u w = rw[j];
         const unsigned sv = rs[j];
+        v4u b[4];
+        dequant(rw[j], mask, magic, b);
         v4f d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) d = mfma_bf16(a[i], dequant(w[i], mask, magic), d);
+        for (int i = 0; i < 4; ++i) d = mfma_bf16(a[i], b[i], d);
         const float sc = __uint_as_float(sv << 16);
-        const float c = 128.0f + (float)(short)(sv >> 16);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[s2][i] = fmaf(sc, fmaf(-c, xsum[g][i], d[i]), acc[s2][i]);
+        for (int i = 0; i < 4; ++i) acc[s2][i] = fmaf(sc, d[i], acc[s2][i]);
+        if (c4 == g % 4) zs[s2][g / 4] = sv;        // for the zero correction below
         load(next, g, s2);                          // the same tile of the next item
       }
     }
+    // offset and zero: acc -= sum_g xsum[row, g] * scale[g, col] * (128 + zero[g, col]), the
+    // wave's GQ groups as the K of f32 MFMAs (the product of a bf16 scale and an integer
+    // below 2^11 is exact in f32)
+#pragma unroll
+    for (int s2 = 0; s2 < SS; ++s2)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const unsigned sv = zs[s2][j];
+        const float z = __uint_as_float(sv << 16) * (128.0f + (float)(short)(sv >> 16));
+        acc[s2] = __builtin_amdgcn_mfma_f32_16x16x4f32(xs_a[j], z, acc[s2], 0, 0, 0);
+      }
     // K splits -> the split-0 wave of the item, in split order; the buffer is single, so a
     // second barrier keeps the next pass's writes behind this pass's reads
     if (SKW > 1) {
@@ -192,6 +251,7 @@ int rlu_gemm_w4_m16(const void* x, int M, int K, const void* wq, const unsigned*
   using namespace rlu::w4;
   if (M < 1 || M > 16 || K <= 0 || N <= 0 || wv < 0 || wv > 16) return -1;
   if (K % 128 || N % (16 * SS) || K > MAXK) return -2;
+  if ((long long)N * K / 2 >= (1LL << 31)) return -2;   // buffer byte offsets are 32-bit
   const int G = K / 128;
   const int skw = G % 4 == 0 ? 4 : G % 2 == 0 ? 2 : 1;
   const int gq = G / skw;
