@@ -14,7 +14,8 @@ with routed weights, moe_sum -- captured once as a HIP graph and replayed with n
 pinned host memory over PCIe, is timed in a second graph and reported as
 `e2e_with_gather_ms_per_step` (the gather overlapped with the GEMMs of the rows already
 resident; `e2e_no_overlap_ms_per_step` is the same steps with the gather in front of every
-GEMM); the same step at B=1 (5 tokens) is `b1_ms_per_step`. The
+GEMM); the same step at B=1 (5 tokens) is `b1_ms_per_step`, with the gather
+`b1_e2e_with_gather_ms_per_step`. The
 static hot/cold arm (inserts disabled: the warm-start set stays resident and every other
 routed expert is read over PCIe by the GEMMs, every step) is `e2e_static_arm_ms_per_step`.
 
@@ -638,7 +639,7 @@ def main():
         torch.cuda.synchronize()
         # B=1: same layers' slots, fresh caches, 5 tokens
         rows1 = 5
-        layers1, ids1 = build(torch, pkg, rows1, args.warmup + args.steps + 1, dev, None,
+        layers1, ids1 = build(torch, pkg, rows1, args.warmup + 2 * args.steps + 2, dev, None,
                               host_full, layers_cache=layers4)
         tw1 = torch.softmax(torch.randn(rows1, TOPK, generator=g), -1).to(dev)
         hb1 = torch.empty((LAYERS + 1, rows1, H), dtype=torch.bfloat16, device=dev)
@@ -651,7 +652,18 @@ def main():
         ms1, _ = time_steps(torch, g1, ids1_dev, ids1_static, args.warmup, args.steps)
         out["b1_ms_per_step"] = round(ms1, 4)
         log(f"B=1 HBM-resident step: {ms1:.3f} ms")
-        del g1, layers1
+        del g1
+        torch.cuda.synchronize()
+        # the same B=1 steps with the miss gather (overlapped) in the graph
+        t1 = args.warmup + args.steps
+        g1e = capture(torch, layers1, ids1_static, tw1, hb1, gather=True, side=side)
+        run_steps(torch, g1e, ids1_dev, ids1_static, t1, 1)
+        ms1e, _ = time_steps(torch, g1e, ids1_dev, ids1_static, t1 + 1, args.steps)
+        out["b1_e2e_with_gather_ms_per_step"] = round(ms1e, 3)
+        out["b1_misses_per_layer_last_step"] = round(
+            float(np.mean([int(L.cache.n_miss.item()) for L in layers1])), 2)
+        log(f"B=1 with PCIe miss gather: {ms1e:.3f} ms")
+        del g1e, layers1
         torch.cuda.synchronize()
         out["lm_head_fp8"] = lm_head_fp8(torch, pkg, dev)
         log(f"fp8 lm_head M=5: {out['lm_head_fp8']['us']} us")
