@@ -9,16 +9,20 @@ Mirrors the reference's Python entry points for these stages:
                                   363-423), same argument list; ws_t = [E, N/128, K/128] fp32
                                   block scales, x_scale = [rows, K/128]; wref unused
   gemm_fp8_block                  kernels/fp8_target_lmhead.py:70-74
+  Fp8TargetHead                   kernels/fp8_target_lmhead.py:77-93
   shuffle_fp8_weight              shuffle_weight_gfx1201 (kernels/fp8_target_lmhead.py:47,64),
                                   here the gfx950 MFMA fragment order every GEMM reads
   pack_fp8_block                  kernels/fp8_target_lmhead.py:44-66
   moe_gemm_tiled                  the grouped GEMM for prefill-sized inputs (no counterpart:
                                   the reference ran one closed kernel at every M)
-Errors from the C-ABI raise RuntimeError; there is no fallback implementation.
+Errors from the C-ABI raise RuntimeError; there is no fallback implementation (Fp8TargetHead
+hands the calls its kernel does not take to the caller's own lm_head method, as the
+reference's does).
 """
 from __future__ import annotations
 
 import ctypes
+import os
 
 import torch
 
@@ -109,24 +113,58 @@ def _r4d_fp8_moe_gemm_into(y: torch.Tensor, qx: torch.Tensor, x_scale: torch.Ten
 def gemm_fp8_block_q(qx: torch.Tensor, xs: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor,
                      out: torch.Tensor | None = None, wv: int = 0, npw: int = 0) -> torch.Tensor:
     """e4m3 [M, K] (xs [M, K/128]) x e4m3 [N, K] in fragment order (ws [N/128, K/128])^T ->
-    bf16 [M, N]. npw = 0 picks the tile width measured fastest at vocab 151936 x 2560: two
-    16-column tiles per item up to M = 8, four above."""
+    bf16 [M, N], one launch per 16 rows. npw = 0 picks the tile width measured fastest at
+    vocab 151936 x 2560: two 16-column tiles per item up to 8 rows, four above."""
     M, K = qx.shape
-    if npw == 0:
-        npw = 2 if M <= 8 else 4
     N = wq.shape[0]
+    assert qx.is_contiguous() and xs.is_contiguous() and xs.shape == (M, K // GROUP)
     y = torch.empty((M, N), dtype=torch.bfloat16, device=qx.device) if out is None else out
-    rc = lib().rlu_gemm_fp8blk_m16(_p(qx), _p(xs), _p(wq), _p(ws), _p(y), M, N, K, wv, npw,
-                                   _P(stream_ptr()))
-    check(rc, "rlu_gemm_fp8blk_m16")
+    assert y.shape == (M, N) and y.is_contiguous()
+    for r0 in range(0, M, 16):
+        m = min(M, r0 + 16) - r0
+        p = npw if npw else (2 if m <= 8 else 4)
+        rc = lib().rlu_gemm_fp8blk_m16(_P(qx[r0].data_ptr()), _P(xs[r0].data_ptr()), _p(wq),
+                                       _p(ws), _P(y[r0].data_ptr()), m, N, K, wv, p,
+                                       _P(stream_ptr()))
+        check(rc, "rlu_gemm_fp8blk_m16")
     return y
 
 
 def gemm_fp8_block(x: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor) -> torch.Tensor:
     """bf16 [M, K] @ dequant(W)^T -> bf16 [M, N]: group-128 activation quant, then the GEMM
-    (kernels/fp8_target_lmhead.py:70-74); M <= 16."""
+    (kernels/fp8_target_lmhead.py:70-74), 16 rows per launch."""
     qx, xs = fp8_quant_group(x.contiguous(), GROUP)
     return gemm_fp8_block_q(qx, xs, wq, ws)
+
+
+# decode rows the fp8 head takes; larger batches go to the original method
+# (kernels/fp8_target_lmhead.py:31)
+FP8_LMHEAD_MAX_M = int(os.environ.get("VLLM_TARGET_FP8_LMHEAD_MAX_M", "64"))
+
+
+class Fp8TargetHead:
+    """Drop-in replacement for the lm_head's quant_method at decode M
+    (kernels/fp8_target_lmhead.py:77-93). The weight is packed once (pack_fp8_block). apply()
+    runs gemm_fp8_block for bf16 inputs of at most FP8_LMHEAD_MAX_M rows and no bias, and
+    hands every other call, and every other attribute, to the original method."""
+
+    def __init__(self, orig_method, weight: torch.Tensor):
+        self.orig = orig_method
+        self.wq, self.ws = pack_fp8_block(weight)
+        self.n_fp8 = 0                              # calls served by the fp8 kernel
+
+    def apply(self, layer, x: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
+        flat = x.reshape(-1, x.shape[-1])
+        if flat.shape[0] > FP8_LMHEAD_MAX_M or bias is not None or x.dtype != torch.bfloat16:
+            return self.orig.apply(layer, x, bias=bias)
+        y = gemm_fp8_block(flat, self.wq, self.ws)
+        self.n_fp8 += 1
+        return y.reshape(*x.shape[:-1], y.shape[-1])
+
+    def __getattr__(self, name):
+        if name == "orig":                          # not set yet (copy / unpickle)
+            raise AttributeError(name)
+        return getattr(self.orig, name)
 
 
 def shuffle_fp8_weight(w: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:

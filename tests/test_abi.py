@@ -67,3 +67,35 @@ def test_missing_library_fails_loudly(pkg, monkeypatch, tmp_path):
             pkg._lib.lib()
     finally:
         pkg._lib.lib.cache_clear()
+
+
+def test_fp8_target_head_routes_without_a_gpu(pkg):
+    """Fp8TargetHead's dispatch (kernels/fp8_target_lmhead.py:85-93), host side only: more rows
+    than VLLM_TARGET_FP8_LMHEAD_MAX_M, a bias, or a non-bf16 input go to the original method;
+    attributes it does not define come from the original method."""
+    import torch
+    from importlib import import_module
+    ops = import_module(pkg.__name__ + ".ops")
+
+    class Orig:
+        tag = "orig-attr"
+
+        def __init__(self):
+            self.calls = []
+
+        def apply(self, layer, x, bias=None):
+            self.calls.append((tuple(x.shape), x.dtype, bias is not None))
+            return "orig"
+
+    head = ops.Fp8TargetHead.__new__(ops.Fp8TargetHead)
+    head.orig, head.wq, head.ws, head.n_fp8 = Orig(), None, None, 0
+    m = ops.FP8_LMHEAD_MAX_M
+    assert m == 64
+    assert head.apply(None, torch.zeros(m + 1, 128, dtype=torch.bfloat16)) == "orig"
+    assert head.apply(None, torch.zeros(2, 3, 128, dtype=torch.bfloat16),
+                      bias=torch.zeros(8)) == "orig"
+    assert head.apply(None, torch.zeros(4, 128, dtype=torch.float16)) == "orig"
+    assert [c[0] for c in head.orig.calls] == [(m + 1, 128), (2, 3, 128), (4, 128)]
+    assert head.n_fp8 == 0 and head.tag == "orig-attr"
+    with pytest.raises(AttributeError):
+        ops.Fp8TargetHead.__new__(ops.Fp8TargetHead).anything

@@ -583,3 +583,61 @@ def test_moe_gemm_tiled_row_contract_and_graph(ops, layer):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(y2.view(torch.int16), y.view(torch.int16))
+
+
+class _OrigHead:
+    """Stand-in for the lm_head's original quant method: records calls, returns a marker."""
+
+    def __init__(self):
+        self.calls = []
+        self.tag = "orig-attr"
+
+    def apply(self, layer, x, bias=None):
+        self.calls.append((tuple(x.shape), x.dtype, bias is not None))
+        return "orig"
+
+
+def test_fp8_target_head(ops, lm_head):
+    """Fp8TargetHead (kernels/fp8_target_lmhead.py:77-93): batched bf16 input of up to 64 rows
+    goes through gemm_fp8_block in 16-row launches (rows of a full slice equal a direct 16-row
+    call bit for bit; all rows within 1e-2 of the float64 dequant reference); more rows, a
+    bias or another dtype go to the original method; other attributes pass through."""
+    wq, ws, wt = lm_head
+    N, K = wq.shape
+    head = ops.Fp8TargetHead.__new__(ops.Fp8TargetHead)
+    head.orig, head.wq, head.ws, head.n_fp8 = _OrigHead(), wt, ws, 0
+    rng = np.random.default_rng(40)
+    x = fp8.bf16_round(rng.standard_normal((2, 20, K)).astype(np.float32))
+    xt = bf16_from_np(x.reshape(40, K)).reshape(2, 20, K)
+    gpu_case("fp8 target head M=40")
+    y = head.apply(None, xt)
+    y16 = ops.gemm_fp8_block(xt.reshape(40, K)[16:32], wt, ws)
+    torch.cuda.synchronize()
+    assert y.shape == (2, 20, N) and head.n_fp8 == 1 and not head.orig.calls
+    assert torch.equal(y.reshape(40, N)[16:32].view(torch.int16), y16.view(torch.int16))
+    qx, xs = fp8.group_quant(x.reshape(40, K), 128)
+    a = torch.from_numpy(fp8.dequant_act(qx, xs)).to(DEV).double()
+    wd = (wq.float() * ws.repeat_interleave(128, 0).repeat_interleave(128, 1)).double()
+    ref = a @ wd.T
+    del wd
+    err = ((y.reshape(40, N).double() - ref).abs().max() / ref.abs().max()).item()
+    assert err <= TOL, f"rel err {err:.3e}"
+    # routed to the original method
+    big = torch.zeros((65, K), dtype=torch.bfloat16, device=DEV)
+    assert head.apply(None, big) == "orig"
+    assert head.apply(None, xt, bias=torch.zeros(N, device=DEV)) == "orig"
+    assert head.apply(None, xt.float()) == "orig"
+    assert [c[0] for c in head.orig.calls] == [(65, K), (2, 20, K), (2, 20, K)]
+    assert head.n_fp8 == 1 and head.tag == "orig-attr"
+
+
+def test_fp8_target_head_packs_its_weight(ops):
+    """The constructor packs the weight exactly as pack_fp8_block does."""
+    g = torch.Generator(device=DEV).manual_seed(3)
+    w = (torch.randn(256, 384, device=DEV, generator=g) * 0.05).to(torch.bfloat16)
+    gpu_case("fp8 target head pack")
+    head = ops.Fp8TargetHead(_OrigHead(), w)
+    wt, ws = ops.pack_fp8_block(w)
+    torch.cuda.synchronize()
+    assert torch.equal(head.wq.view(torch.uint8), wt.view(torch.uint8))
+    assert torch.equal(head.ws, ws)
