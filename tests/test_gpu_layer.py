@@ -245,3 +245,45 @@ def test_layer_overlap_graph_replay(pkg, pool):
         torch.cuda.synchronize()
     assert installs > 0, "the trace must install experts"
     del g
+
+
+def test_layer_overlap_read_through_and_cold_rows(pkg, pool):
+    """Overlap across read-through steps (more distinct experts than the gate: no install, the
+    non-resident experts run cold in the overlapped phase) alternating with insert steps:
+    outputs and states equal the serial order bit for bit, and the oracle within 2e-2."""
+    M = 20
+    ta, perm0 = trace.zipf_trace(seed=420, E=E, rows=M, k=TOPK, steps=4, s=1.1, corr=0.7)
+    tb, _ = trace.zipf_trace(seed=500, E=E, rows=M, k=TOPK, steps=4, s=0.6)
+    mix = np.stack([ta[0], tb[0], ta[1], tb[1], ta[2]]).reshape(5, M, TOPK).astype(np.int32)
+    hot, rank = trace.warm_hot(perm0, S)
+    full = pkg.ExpertWeights(pool["w13"], pool["w13s"], pool["w2"], pool["w2s"])
+    a = pkg.LruMoELayer(full, hot, rank, M, TOPK, DEV)
+    b = pkg.LruMoELayer(full, hot, rank, M, TOPK, DEV)
+    st = olru.warm_start(E, S, hot, rank)
+    rng = np.random.default_rng(420)
+    side = torch.cuda.Stream()
+    kinds = []
+    for t in range(mix.shape[0]):
+        ids = mix[t]
+        x = fp8.bf16_round(rng.standard_normal((M, H)).astype(np.float32))
+        tw = rng.random((M, TOPK)).astype(np.float32)
+        xd = torch.from_numpy(x).to(torch.bfloat16).to(DEV)
+        twd, idd = torch.from_numpy(tw).to(DEV), torch.from_numpy(ids).to(DEV)
+        oa = torch.empty((M, H), dtype=torch.bfloat16, device=DEV)
+        ob = torch.empty_like(oa)
+        gpu_case(f"overlap read-through mix step {t}")
+        a.apply(oa, xd, twd, idd, gather=True, side=side, overlap=True)
+        b.apply(ob, xd, twd, idd, gather=True, side=side, overlap=False)
+        torch.cuda.synchronize()
+        olru.fused(st, ids.reshape(-1), 16)
+        cold = int((st.map_cold[ids.reshape(-1)] >= 0).sum())
+        kinds.append((int(st.n_miss[0]), cold))
+        assert torch.equal(oa.view(torch.int16), ob.view(torch.int16)), f"step {t}"
+        for name, ga in zip(olru.LruState.NAMES, a.cache.state()):
+            if name == "routed":
+                continue
+            assert np.array_equal(ga.cpu().numpy(), getattr(st, name)), (t, name)
+        err = ogemm.rel_err(oa.float().cpu().numpy(), oracle_layer(x, ids, tw, pool))
+        assert err <= TOL, f"step {t}: rel err {err:.3e}"
+    assert any(n > 0 and c == 0 for n, c in kinds), kinds      # insert steps
+    assert any(n == 0 and c > 0 for n, c in kinds), kinds      # read-through, cold rows
