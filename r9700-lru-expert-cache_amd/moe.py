@@ -63,11 +63,12 @@ class ExpertWeights:
 class LruMoELayer:
     def __init__(self, full: ExpertWeights, hot_ids, rank: dict | None, max_tokens: int,
                  top_k: int, device="cuda", slots: ExpertWeights | None = None,
-                 npw1: int = 2, npw2: int = 4, sk1: int = 2, sk2: int = 1, wv: int = 0,
-                 max_inserts: int | None = None):
+                 npw1: int = 2, npw2: int = 4, sk1: int | None = None, sk2: int = 1,
+                 wv: int = 0, max_inserts: int | None = None):
         """npw / sk: 16-column tiles per item and K split of gate_up (1) and down (2); the
         defaults are the fastest measured at the decode shapes (hidden 2560, intermediate
-        768, 5-20 tokens). max_inserts: cap on cache inserts per step (default
+        768): gate_up splits K over 2 waves above 8 tokens (20 tokens: 3.70 vs 3.95 ms per
+        52-layer step) and not at all up to 8 (5 tokens: 3.007 vs 3.038 ms). max_inserts: cap on cache inserts per step (default
         VLLM_R4D_LRU_MAX_INSERTS, 64); 0 is the static hot/cold arm -- the warm-start set stays
         resident and every other routed expert is read from the full tensor
         (r4d_mxfp4_moe.py.static.diff, and the README's MAX_INSERTS=0 ablation)."""
@@ -80,6 +81,8 @@ class LruMoELayer:
         self.top_k = top_k
         self.M = max_tokens
         self.mtk = max_tokens * top_k
+        if sk1 is None:
+            sk1 = 1 if max_tokens <= 8 else 2
         self.npw1, self.npw2, self.sk1, self.sk2, self.wv = npw1, npw2, sk1, sk2, wv
         for t in full.tensors():
             slab = t[0].numel() * t.element_size()
