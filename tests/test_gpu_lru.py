@@ -439,3 +439,85 @@ def test_split_fresh_clamps_to_the_miss_capacity(pkg):
         assert lib.rlu_lru_split_fresh(P(eids.data_ptr()), nb, P(miss.data_ptr()),
                                        P(n_miss.data_ptr()), cap, S, P(res.data_ptr()),
                                        P(new.data_ptr()), None) == -1
+
+
+def test_multilayer_graph_fused_and_gather(pkg, mine):
+    """tests/lru/test_graph_lru.py:102-158: several layers of (fused manager + align, then the
+    miss gather on a side stream) captured as one HIP graph and replayed 20 times with new
+    routing: after every replay each layer's cache state and align outputs equal the oracle's,
+    and every slot of every layer holds its expert's bytes in all six buffers (the slot
+    audit of tests/lru/test_slots_prod.py:199-207)."""
+    L, E, S, rows, steps = 8, 128, 64, 5, 21
+    sizes = [4096, 2048, 64, 32, 64, 32]
+    g = torch.Generator().manual_seed(5)
+    src_h, src_d = [], []
+    for b in sizes:
+        h, dp = _uva(E * b)
+        h.copy_(torch.randint(0, 256, (E * b,), dtype=torch.uint8, generator=g))
+        src_h.append(h.view(E, b))
+        src_d.append(dp)
+    layers = []
+    for l in range(L):
+        tr, perm0 = pkg.traces.zipf_trace(seed=700 + l, E=E, rows=rows, k=10, steps=steps,
+                                          s=1.1)
+        hot, rank = pkg.traces.warm_hot(perm0, S)
+        st = olru.warm_start(E, S, hot, rank, thresh=1.0)    # 5-10 inserts a step
+        d = to_dev(st)
+        slots = [torch.empty((S, b), dtype=torch.uint8, device=DEV) for b in sizes]
+        idx = torch.from_numpy(st.slot_expert.astype(np.int64))
+        for i in range(6):
+            slots[i].copy_(src_h[i].index_select(0, idx))
+        layers.append(dict(tr=tr, st=st, d=d, slots=slots, out=new_out(rows * 10, E),
+                           ids=torch.zeros(rows * 10, dtype=torch.int32, device=DEV)))
+    side = torch.cuda.Stream()
+
+    def step():
+        cur = torch.cuda.current_stream()
+        for ly in layers:
+            call(mine, "fused", ly["ids"], ly["d"], ly["st"].max_distinct, ly["st"].max_inserts,
+                 ly["out"])
+            side.wait_stream(cur)
+            with torch.cuda.stream(side):
+                pkg._r4d_lru_gather(ly["slots"], src_h, ly["d"]["miss"], ly["d"]["n_miss"], 4,
+                                    32, src_ptrs=src_d)
+            cur.wait_stream(side)
+
+    def check(n, tag):
+        inserts = 0
+        for l, ly in enumerate(layers):
+            want = olru.fused(ly["st"], ly["tr"][n], BS)
+            inserts += int(ly["st"].n_miss[0])
+            assert_state(ly["d"], ly["st"], f"{tag} layer {l}", skip=())
+            for i, (gg, w) in enumerate(zip(ly["out"], want)):
+                assert np.array_equal(gg.cpu().numpy(), w), f"{tag} layer {l}: output {i}"
+            idx = torch.from_numpy(ly["st"].slot_expert.astype(np.int64))
+            for i in range(6):
+                assert torch.equal(ly["slots"][i].cpu(), src_h[i].index_select(0, idx)), \
+                    f"{tag} layer {l}: buffer {i}"
+        return inserts
+
+    # step 0 eager on a side stream (loads the kernels), then capture, then 20 replays
+    gpu_case("multi-layer graph: eager step 0")
+    for ly in layers:
+        ly["ids"].copy_(torch.from_numpy(ly["tr"][0]))
+    s0 = torch.cuda.Stream()
+    s0.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s0):
+        step()
+    torch.cuda.current_stream().wait_stream(s0)
+    torch.cuda.synchronize()
+    check(0, "eager step 0")
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        step()
+    torch.cuda.synchronize()
+    total = 0
+    for n in range(1, steps):
+        gpu_case(f"multi-layer graph replay {n}")
+        for ly in layers:
+            ly["ids"].copy_(torch.from_numpy(ly["tr"][n]))
+        gr.replay()
+        torch.cuda.synchronize()
+        total += check(n, f"replay {n}")
+    assert total > 0, "the traces must insert"
+    del gr
