@@ -520,7 +520,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this path runs on one GPU; --gpus must be 1 (multi-GPU "
-                                   "sharding is described in DESIGN.md, not launched)"}))
+                                   "sharding is a design here, not launched)"}))
         sys.exit(2)
     if int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py runs on one GPU only", file=sys.stderr)

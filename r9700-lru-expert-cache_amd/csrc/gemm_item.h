@@ -1,5 +1,5 @@
-// One wave's share of one grouped-GEMM item, shared by the decode kernels (gemm.hip: plain bf16
-// output; gemm_act.hip: SiLU-mul-quant epilogue).
+// One wave's share of one grouped-GEMM item: the core of the decode kernel moe_gemm_k
+// (gemm.hip), for the MoE GEMMs and the fp8 lm_head.
 //
 // An item is (one 16-row block, 16 * NPW output columns starting at n0). SKW waves split its K
 // range; wave ks streams steps [ks * kpw, (ks + 1) * kpw) of every strip through a ring of D
