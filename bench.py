@@ -377,7 +377,25 @@ def prefill_gemm(torch, pkg, dev, T=4096, reps=3):
                                           tiles=tiles, wv=2))
     u2 = timed(lambda: ops.moe_gemm_tiled(y2, x2, s2, w2, w2s, sh, eh, nh, tw, mtk, 1,
                                           tiles=tiles, wv=2))
-    res = {}
+    # the fused LRU + both aligns (+ the group-128 quant of the chunk's hidden states, as the
+    # layer calls it) over the chunk's 40960 (token, k) ids
+    ids_d = torch.from_numpy(ids).to(dev).reshape(-1)
+    hs = torch.randn(T, H, device=dev, generator=g).to(torch.bfloat16)
+    qx = torch.empty(T, H, dtype=torch.uint8, device=dev)
+    qs = torch.empty(T, H // 128, dtype=torch.float32, device=dev)
+    def timed_avg(fn, n=50):
+        fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(n):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) * 1e3 / n
+    ua = timed_avg(lambda: cache.fused(ids_d, out=al))
+    uq = timed_avg(lambda: cache.fused_quant(ids_d, al, hs, qx, qs))
+    res = {"lru_align_us": round(ua, 1), "lru_align_quant_us": round(uq, 1)}
     for name, us, n, k in (("gate_up", u1, 2 * I, H), ("down", u2, H, I)):
         res[name] = dict(us=round(us, 1), tflops=round(2.0 * mtk * n * k / us / 1e6, 1),
                          weight_gbs=round(E * n * k / us / 1e3, 1))

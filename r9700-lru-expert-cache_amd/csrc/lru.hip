@@ -5,8 +5,8 @@
 // lru_fused_k :418-575, lru_gather_k :271-301); the entry points at the bottom keep its C-ABI.
 // The implementation is this build's own, shaped for wave64 CDNA4:
 //
-//  * One workgroup of 256 threads (one wave per SIMD), seven barriers for the fused kernel
-//    (three for the manager). Every global load is issued up front, so the kernel pays one
+//  * One workgroup of 256 threads (one wave per SIMD), seven barriers for the fused kernel at
+//    decode sizes (three for the manager). Every global load is issued up front, so the kernel pays one
 //    memory round trip, not one per phase. Decode-sized align outputs are built in LDS and
 //    written once, coalesced, with the sentinels past num_post_pad written directly; larger
 //    ones are pre-filled with their sentinels in global memory, and only the first barrier
@@ -24,7 +24,8 @@
 //  * Align is stable at every mk: a token's rank inside its bucket is the number of earlier
 //    tokens routed to the same expert -- up to 256 tokens a popcount of the expert's token
 //    bitmap below it (each token places itself), above that a bit-sliced wave match plus
-//    per-wave counts in LDS.
+//    per-wave counts in LDS. Above 2048 tokens the ranking moves to place_k, one workgroup per
+//    1024 tokens, each counting the tokens before its own.
 //
 // Preconditions (checked by the reference's own tests after every step, tests/lru/test_lru.py:
 // 138-145): table/map_cold complementary, table[slot_expert[s]] == s for resident slots,
@@ -48,6 +49,7 @@ constexpr int QS = MAXS / WAVE;      // slot registers per lane in the selecting
 constexpr int EJ = MAXE / NT;        // experts per thread
 constexpr int NWORD = MAXE / 64;     // bitmap words
 
+constexpr int MLOADS = 32;           // id loads in flight per thread when marking > NT tokens
 constexpr int TW = NT / 64;          // u64 words of a per-expert token mask (<= NT tokens)
 constexpr int LSTAGE = 4096;         // align outputs staged in LDS up to this many sorted ids
 constexpr int NBSTAGE = 256;         // ... and this many expert ids, per side
@@ -78,6 +80,30 @@ struct LruLds {
   alignas(16) int stage_c[LSTAGE];
   int stage_eh[NBSTAGE], stage_ec[NBSTAGE];
 };
+
+// cnt[e] += the number of ids[lo, hi) equal to e, for e in [0, E), with VL 16-byte loads in
+// flight per thread (ids + lo 16-byte aligned, hi - lo a multiple of 4). Counts are LDS
+// atomics, so the order of the tokens does not matter.
+constexpr int VL = 16;
+__device__ __forceinline__ void count_ids_vec(const int* __restrict__ ids, int lo, int hi, int E,
+                                              int* cnt) {
+  const int4* v = reinterpret_cast<const int4*>(ids + lo);
+  const int nv = (hi - lo) / 4;
+  for (int j = threadIdx.x; j < nv; j += VL * NT) {
+    int4 a[VL];
+#pragma unroll
+    for (int u = 0; u < VL; ++u) a[u] = v[min(j + u * NT, nv - 1)];
+#pragma unroll
+    for (int u = 0; u < VL; ++u) {
+      if (j + u * NT < nv) {
+        if ((unsigned)a[u].x < (unsigned)E) atomicAdd(&cnt[a[u].x], 1);
+        if ((unsigned)a[u].y < (unsigned)E) atomicAdd(&cnt[a[u].y], 1);
+        if ((unsigned)a[u].z < (unsigned)E) atomicAdd(&cnt[a[u].z], 1);
+        if ((unsigned)a[u].w < (unsigned)E) atomicAdd(&cnt[a[u].w], 1);
+      }
+    }
+  }
+}
 
 __device__ __forceinline__ bool bit_of(const uint64_t* bm, int e) {
   return ((bm[e >> 6] >> (e & 63)) & 1ull) != 0;
@@ -305,8 +331,17 @@ struct Blk {
 // each call site compiles to LDS or global stores (no generic pointers).
 __device__ __forceinline__ void fill_align(int* __restrict__ oh, int* __restrict__ oc,
                                            int* __restrict__ eh, int* __restrict__ ec, int Lsz,
-                                           int NB, int mk) {
-  for (int k = threadIdx.x; k < Lsz; k += NT) {
+                                           int NB, int mk, bool vec) {
+  int k0 = 0;
+  if (vec) {                                        // 16-byte stores (outputs 16-byte aligned)
+    const int4 m4 = make_int4(mk, mk, mk, mk);
+    for (int k = 4 * threadIdx.x; k + 4 <= Lsz; k += 4 * NT) {
+      *reinterpret_cast<int4*>(oh + k) = m4;
+      *reinterpret_cast<int4*>(oc + k) = m4;
+    }
+    k0 = Lsz & ~3;
+  }
+  for (int k = k0 + threadIdx.x; k < Lsz; k += NT) {
     oh[k] = mk;
     oc[k] = mk;
   }
@@ -383,11 +418,12 @@ __device__ __forceinline__ int post_slot(const LruLds& L, int e, int S, int nact
 }
 
 // The per-token-group-128 quant of the layer's hidden state, run by workgroups 1.. of the fused
-// launch (one row each) while workgroup 0 runs the cache: the two are independent and both
-// feed the first GEMM, so one launch serves both.
+// launch while workgroup 0 runs the cache: the two are independent and both feed the first
+// GEMM, so one launch serves both. One row per wave: the launch's LDS footprint leaves room for
+// one workgroup per CU, so a prefill chunk's rows go four to a workgroup.
 struct QuantJob {
   const uint16_t* x;
-  int K, ldx;
+  int rows, K, ldx;
   uint8_t* q;
   float* scale;
 };
@@ -402,11 +438,12 @@ __global__ __launch_bounds__(NT) void lru_k(
     long long* __restrict__ step, int* __restrict__ miss, int* __restrict__ n_miss, int bs,
     int Lsz, int NB, int* __restrict__ sorted_hot, int* __restrict__ eids_hot,
     int* __restrict__ npad_hot, int* __restrict__ sorted_cold, int* __restrict__ eids_cold,
-    int* __restrict__ npad_cold, QuantJob qj, bool vec_out) {
-  if (blockIdx.x > 0) {
-    const int r = blockIdx.x - 1;
-    group_quant_row128(qj.x + (size_t)r * qj.ldx, qj.K, qj.q + (size_t)r * qj.K,
-                       qj.scale + (size_t)r * (qj.K / 128));
+    int* __restrict__ npad_cold, QuantJob qj, bool vec_out, bool defer_place) {
+  if (blockIdx.x > 0) {                          // quant workgroups: one row per wave
+    const int r = (blockIdx.x - 1) * NW + (int)threadIdx.x / WAVE;
+    if (r < qj.rows)
+      wave_quant_row128(qj.x + (size_t)r * qj.ldx, qj.K, qj.q + (size_t)r * qj.K,
+                        qj.scale + (size_t)r * (qj.K / 128));
     return;
   }
   __shared__ LruLds L;
@@ -448,7 +485,7 @@ __global__ __launch_bounds__(NT) void lru_k(
       }
     } else {
       reinterpret_cast<uint4*>(&L.tk.wcnt[0][0])[t] = make_uint4(0, 0, 0, 0);
-      fill_align(sorted_hot, sorted_cold, eids_hot, eids_cold, Lsz, NB, mk);
+      fill_align(sorted_hot, sorted_cold, eids_hot, eids_cold, Lsz, NB, mk, vec_out);
     }
     for (int i = t; i < S; i += NT) L.cnt_h[i] = 0;
   }
@@ -471,10 +508,14 @@ __global__ __launch_bounds__(NT) void lru_k(
   else
     lds_barrier();    // 1
 
-  // ---- mark routed experts and their slots; per-expert token sets -------------------------
-  for (int i = t; i < mk; i += NT) {
-    const int e = i == t ? tok0 : ids[i];
-    if (e >= 0 && e < E) {
+  // ---- mark routed experts and their slots; per-expert token sets. The general align path
+  // only counts tokens per expert here (one atomic per token): its routed and busy-slot
+  // bitmaps follow from the counts after the barrier --------------------------------------
+  const bool count_only = ALIGN && !staged;
+  auto mark = [&](int e, int i) {
+    if (count_only) {
+      if (e >= 0 && e < E) atomicAdd(&L.ecnt[e], 1);
+    } else if (e >= 0 && e < E) {
       atomicOr(reinterpret_cast<unsigned long long*>(&L.rbits[e >> 6]), 1ull << (e & 63));
       const int s = L.tab[e];
       if ((unsigned)s < (unsigned)S)
@@ -487,6 +528,22 @@ __global__ __launch_bounds__(NT) void lru_k(
           atomicAdd(&L.ecnt[e], 1);
       }
     }
+  };
+  if (t < mk) mark(tok0, t);
+  int mark_from = NT;
+  if (count_only && (((uintptr_t)ids & 15) == 0) && mk > NT) {
+    mark_from = NT + ((mk - NT) & ~3);
+    count_ids_vec(ids, NT, mark_from, E, L.ecnt);
+    if (t < mk - mark_from) mark(ids[mark_from + t], mark_from + t);
+    mark_from = mk;
+  }
+  for (int i = t + mark_from; i < mk; i += MLOADS * NT) {  // MLOADS loads in flight
+    int e[MLOADS];
+#pragma unroll
+    for (int u = 0; u < MLOADS; ++u) e[u] = ids[min(i + u * NT, mk - 1)];
+#pragma unroll
+    for (int u = 0; u < MLOADS; ++u)
+      if (i + u * NT < mk) mark(e[u], i + u * NT);
   }
   const int kbits = E > 1 ? 32 - __clz(E - 1) : 0;
   int inrank = 0;
@@ -496,6 +553,19 @@ __global__ __launch_bounds__(NT) void lru_k(
     if (v0 && inrank == 0) L.tk.wcnt[w][tok0] = (uint8_t)__popcll(m);
   }
   lds_barrier();  // 2
+  if (count_only) {
+#pragma unroll
+    for (int j = 0; j < EJ; ++j) {
+      const int e = t + NT * j;
+      const bool r = e < E && L.ecnt[e] > 0;
+      const uint64_t rw = __ballot(r);
+      if (lane == 0) L.rbits[j * NW + w] = rw;
+      if (r && (unsigned)tab[j] < (unsigned)S)
+        atomicOr(reinterpret_cast<unsigned long long*>(&L.sbusy[tab[j] >> 6]),
+                 1ull << (tab[j] & 63));
+    }
+    lds_barrier();  // 2b
+  }
 
   // ---- wave 0: distinct count, miss ranks, victims; the other waves meanwhile do what does
   // not depend on the victims: hit stamps, routed flags, bucket counts of every expert that
@@ -680,6 +750,8 @@ __global__ __launch_bounds__(NT) void lru_k(
     return;
   }
 
+  if (defer_place) return;                        // place_k ranks the tokens in parallel
+
   // ---- general placement, chunk by chunk of NT tokens in index order ---------------------
   for (int c = 0; c * NT < mk; ++c) {
     const int i = c * NT + t;
@@ -791,6 +863,136 @@ __global__ __launch_bounds__(NT) void split_fresh_k(const int* __restrict__ eids
   }
 }
 
+// ---- placement for large token counts, many workgroups ----------------------------------
+// Above PLACE_MIN tokens the fused launch stops once the sentinels, the bucket counts, starts,
+// expert ids and num_post_pad are written; place_k then ranks the tokens. Workgroup c takes
+// tokens [c PC, (c + 1) PC): it counts the earlier tokens per expert with LDS atomics (order
+// does not matter for a count), then ranks its own tokens NT at a time in index order, as the
+// single-workgroup loop does, so every bucket still lists its tokens in ascending index order.
+// A routed expert's bucket is its slot in the updated table (hot) or itself (cold); a bucket
+// starts at the first block of its run in eids_hot / eids_cold. The host takes this route only
+// when NB * bs >= L: then every bucket that starts below L has its first block recorded, and
+// the others (start left at L) place nothing.
+constexpr int PC = 1024;            // tokens ranked by one placement workgroup
+constexpr int PLACE_MIN = 2048;     // the fused launch defers placement above this many tokens
+constexpr int PLOADS = 16;          // id loads in flight per thread while counting (unaligned)
+constexpr int PB = 8;               // expert-id blocks per thread in flight
+
+struct PlaceLds {
+  int start_h[MAXS];
+  int start_c[MAXE];
+  int cnt[MAXE];                    // tokens of the expert before the NT tokens being ranked
+  int tab[MAXE];                    // updated table
+  alignas(16) uint8_t wcnt[NW][MAXE];  // tokens of the expert per wave among those NT tokens
+};
+
+__global__ __launch_bounds__(NT) void place_k(const int* __restrict__ ids, int mk, int E, int S,
+                                              const int* __restrict__ table,
+                                              const int* __restrict__ eids_hot,
+                                              const int* __restrict__ eids_cold, int NB, int bs,
+                                              int Lsz, int* __restrict__ sorted_hot,
+                                              int* __restrict__ sorted_cold) {
+  __shared__ PlaceLds P;
+  const int t = threadIdx.x, w = t / WAVE;
+  const int c0 = blockIdx.x * PC, c1 = min(c0 + PC, mk);
+  // this workgroup's ids and the table first: nothing below waits on a load it does not need
+  constexpr int PU = PC / NT;
+  int own[PU];
+#pragma unroll
+  for (int u = 0; u < PU; ++u) own[u] = ids[min(c0 + t + u * NT, c1 - 1)];
+  int tb[EJ];
+#pragma unroll
+  for (int j = 0; j < EJ; ++j) tb[j] = table[min(t + NT * j, E - 1)];
+  for (int k = t; k < S; k += NT) P.start_h[k] = Lsz;
+#pragma unroll
+  for (int j = 0; j < EJ; ++j) {
+    const int e = t + NT * j;
+    if (e < E) {
+      P.start_c[e] = Lsz;
+      P.cnt[e] = 0;
+      P.tab[e] = tb[j];
+    }
+  }
+  reinterpret_cast<uint4*>(&P.wcnt[0][0])[t] = make_uint4(0, 0, 0, 0);   // NW * MAXE bytes
+  lds_barrier();
+  // the first block of each bucket's run; PB blocks per thread in flight
+  for (int b0 = 0; b0 < NB; b0 += PB * NT) {
+    int eh[PB], ec[PB], ph[PB], pc[PB];
+#pragma unroll
+    for (int u = 0; u < PB; ++u) {
+      const int b = min(b0 + t + u * NT, NB - 1), bp = max(b - 1, 0);
+      eh[u] = eids_hot[b];
+      ec[u] = eids_cold[b];
+      ph[u] = eids_hot[bp];
+      pc[u] = eids_cold[bp];
+    }
+#pragma unroll
+    for (int u = 0; u < PB; ++u) {
+      const int b = b0 + t + u * NT;
+      if (b < NB) {
+        if ((unsigned)eh[u] < (unsigned)S && (b == 0 || eh[u] != ph[u])) P.start_h[eh[u]] = b * bs;
+        if ((unsigned)ec[u] < (unsigned)E && (b == 0 || ec[u] != pc[u])) P.start_c[ec[u]] = b * bs;
+      }
+    }
+  }
+  // the tokens before this workgroup's, per expert
+  const bool vec = (((uintptr_t)ids & 15) == 0);
+  if (vec) count_ids_vec(ids, 0, c0, E, P.cnt);     // c0 is a multiple of 4
+  for (int i = t; !vec && i < c0; i += PLOADS * NT) {
+    int e[PLOADS];
+#pragma unroll
+    for (int u = 0; u < PLOADS; ++u) e[u] = ids[min(i + u * NT, c0 - 1)];
+#pragma unroll
+    for (int u = 0; u < PLOADS; ++u)
+      if (i + u * NT < c0 && (unsigned)e[u] < (unsigned)E) atomicAdd(&P.cnt[e[u]], 1);
+  }
+  lds_barrier();
+  const int kbits = E > 1 ? 32 - __clz(E - 1) : 0;
+#pragma unroll
+  for (int u = 0; u < PU; ++u) {
+    if (c0 + u * NT >= c1) break;                   // uniform over the workgroup
+    const int i = c0 + u * NT + t;
+    const int e = i < c1 ? own[u] : -1;
+    const bool v = (unsigned)e < (unsigned)E;
+    const uint64_t m = match_any(e, v, kbits);
+    const int inrank = mbcnt(m);
+    if (v && inrank == 0) P.wcnt[w][e] = (uint8_t)__popcll(m);
+    lds_barrier();
+    if (v) {
+      int rank = P.cnt[e] + inrank;
+      for (int ww = 0; ww < w; ++ww) rank += P.wcnt[ww][e];
+      const int s = P.tab[e];
+      const bool hot = (unsigned)s < (unsigned)S;
+      const int pos = (hot ? P.start_h[s] : P.start_c[e]) + rank;
+      if (pos < Lsz) {
+        if (hot)
+          sorted_hot[pos] = i;
+        else
+          sorted_cold[pos] = i;
+      }
+    }
+    lds_barrier();
+    if (v && inrank == 0) {                         // fold this wave's count, clear its entry
+      atomicAdd(&P.cnt[e], __popcll(m));
+      P.wcnt[w][e] = 0;
+    }
+    lds_barrier();
+  }
+}
+
+// Placement moves to place_k for large token counts when every bucket start below L is
+// recorded in the block ids (NB blocks of bs cover L).
+static inline bool defer_placement(int mk, int bs, int L, int NB) {
+  return mk > PLACE_MIN && (long long)NB * bs >= L;
+}
+
+static inline void launch_place(const int* ids, int mk, int E, int S, const int* table,
+                                const int* eids_hot, const int* eids_cold, int NB, int bs, int L,
+                                int* sorted_hot, int* sorted_cold, hipStream_t stream) {
+  hipLaunchKernelGGL(place_k, dim3((mk + PC - 1) / PC), dim3(NT), 0, stream, ids, mk, E, S,
+                     table, eids_hot, eids_cold, NB, bs, L, sorted_hot, sorted_cold);
+}
+
 }  // namespace rlu
 
 extern "C" {
@@ -805,7 +1007,7 @@ int r4d_lru_manage(const int* topk_ids, int mk, int E, int S, int max_distinct,
   hipLaunchKernelGGL(rlu::lru_k<false>, dim3(1), dim3(rlu::NT), 0, stream, topk_ids, mk, E, S,
                      max_distinct, max_inserts, table, map_cold, slot_expert, slot_stamp,
                      routed, step, miss, n_miss, 1, 0, 0, nullptr, nullptr, nullptr, nullptr,
-                     nullptr, nullptr, rlu::QuantJob{}, false);
+                     nullptr, nullptr, rlu::QuantJob{}, false, false);
   return (int)hipGetLastError();
 }
 
@@ -819,11 +1021,15 @@ int r4d_lru_fused(const int* topk_ids, int mk, int E, int S, int max_distinct,
   if (E <= 0 || E > rlu::MAXE || S <= 0 || S > rlu::MAXS) return -1;
   if (bs <= 0 || L <= 0 || NB <= 0 || mk < 0) return -1;
   if (max_inserts < 0 || max_inserts > rlu::MAXINS) return -1;
+  const bool defer = rlu::defer_placement(mk, bs, L, NB);
   auto k = bs == 16 ? rlu::lru_k<true, 16> : rlu::lru_k<true, 0>;
   hipLaunchKernelGGL(k, dim3(1), dim3(rlu::NT), 0, stream, topk_ids, mk, E, S, max_distinct,
                      max_inserts, table, map_cold, slot_expert, slot_stamp, routed, step, miss,
                      n_miss, bs, L, NB, sorted_hot, eids_hot, npad_hot, sorted_cold, eids_cold,
-                     npad_cold, rlu::QuantJob{}, rlu::aligned16(sorted_hot, sorted_cold));
+                     npad_cold, rlu::QuantJob{}, rlu::aligned16(sorted_hot, sorted_cold), defer);
+  if (defer)
+    rlu::launch_place(topk_ids, mk, E, S, table, eids_hot, eids_cold, NB, bs, L, sorted_hot,
+                      sorted_cold, stream);
   return (int)hipGetLastError();
 }
 
@@ -842,13 +1048,18 @@ int rlu_lru_fused_quant(const int* topk_ids, int mk, int E, int S, int max_disti
   if (max_inserts < 0 || max_inserts > rlu::MAXINS) return -1;
   if (rows < 0 || K <= 0 || ldx < K || (rows > 0 && (!x || !q || !scale))) return -1;
   if (K % 128 || ldx % 8) return -2;
+  const bool defer = rlu::defer_placement(mk, bs, L, NB);
   auto k = bs == 16 ? rlu::lru_k<true, 16> : rlu::lru_k<true, 0>;
-  hipLaunchKernelGGL(k, dim3(1 + rows), dim3(rlu::NT), 0, stream, topk_ids, mk, E, S,
+  hipLaunchKernelGGL(k, dim3(1 + (rows + rlu::NW - 1) / rlu::NW), dim3(rlu::NT), 0, stream,
+                     topk_ids, mk, E, S,
                      max_distinct, max_inserts, table, map_cold, slot_expert, slot_stamp,
                      routed, step, miss, n_miss, bs, L, NB, sorted_hot, eids_hot, npad_hot,
                      sorted_cold, eids_cold, npad_cold,
-                     rlu::QuantJob{(const uint16_t*)x, K, ldx, (uint8_t*)q, scale},
-                     rlu::aligned16(sorted_hot, sorted_cold));
+                     rlu::QuantJob{(const uint16_t*)x, rows, K, ldx, (uint8_t*)q, scale},
+                     rlu::aligned16(sorted_hot, sorted_cold), defer);
+  if (defer)
+    rlu::launch_place(topk_ids, mk, E, S, table, eids_hot, eids_cold, NB, bs, L, sorted_hot,
+                      sorted_cold, stream);
   return (int)hipGetLastError();
 }
 

@@ -233,6 +233,55 @@ def test_fused_geometries(mine, rows):
         assert np.array_equal(tok, np.arange(ids.size))
 
 
+PLACE_CASES = [
+    # (tag, mk, bs, L override, NB override, invalid-id fraction)
+    ("just-past-threshold", 2049, 16, None, None, 0.0),
+    ("ragged-with-invalid-ids", 9001, 16, None, None, 0.05),
+    # fewer expert-id blocks than L needs (the library bounds the writes; the reference
+    # writes past them): the single-workgroup placement
+    ("L-past-the-blocks", 9000, 16, 9000 + 512 * 15, 100, 0.0),
+    ("runtime-bs-64", 5000, 64, None, None, 0.02),
+    ("ids-not-16-byte-aligned", 7003, 16, None, None, 0.01),
+]
+
+
+@pytest.mark.parametrize("case", PLACE_CASES, ids=[c[0] for c in PLACE_CASES])
+def test_fused_parallel_placement(mine, case):
+    """Above 2048 tokens the align's tokens are ranked by many workgroups; the outputs and the
+    state stay bit-exact against the oracle: ids outside [0, E) skipped, a runtime block size,
+    and a short expert-id array (NB * bs < L), which keeps the single-workgroup placement."""
+    tag, mk, bs, L, NB, bad = case
+    E, S = 512, 257
+    rng = np.random.default_rng(11)
+    _, s = victim_case(E=E, S=S, mk=10, k_cold=0, maxi=64, seed=5)
+    s.max_distinct = E
+    d = to_dev(s)
+    L0, NB0 = olru.align_sizes(mk, E, bs)
+    L, NB = L or L0, NB or NB0
+    for n in range(3):
+        pool = rng.choice(E, 350, replace=False)      # leaves unrouted residents to evict
+        ids = rng.choice(pool, mk).astype(np.int32)
+        nbad = int(bad * mk)
+        if nbad:
+            at = rng.choice(mk, nbad, replace=False)
+            ids[at] = rng.choice(np.array([-1, E, E + 7, -100], np.int32), nbad)
+        want = olru.fused(s, ids, bs, L=L, NB=NB)
+        out = [torch.full((n_,), -12345, dtype=torch.int32, device=DEV)
+               for n_ in (L, NB, 1, L, NB, 1)]
+        gpu_case(f"placement {tag} mk={mk} bs={bs} L={L} NB={NB} step {n}")
+        ids_t = torch.from_numpy(ids).to(DEV)
+        if "aligned" in tag:                          # a view one element into its buffer
+            buf = torch.zeros(mk + 1, dtype=torch.int32, device=DEV)
+            buf[1:] = ids_t
+            ids_t = buf[1:]
+            assert ids_t.data_ptr() % 16 == 4
+        call(mine, "fused", ids_t, d, s.max_distinct, s.max_inserts, out, bs=bs)
+        torch.cuda.synchronize()
+        assert_state(d, s, f"{tag} step {n}", skip=())
+        for i, (g, w) in enumerate(zip(out, want)):
+            assert np.array_equal(g.cpu().numpy(), w), f"{tag} step {n}: output {i}"
+
+
 def test_fused_edges(mine):
     """tests/lru/test_fused.py:282-293: forced read-through and a zero-miss replay."""
     ids_all, s = c1_trace()
@@ -342,10 +391,11 @@ def test_gather_rejects_bad_sizes(pkg):
         pkg._r4d_lru_gather([d] * 6, [d] * 6, m, nm, 0, 16)
 
 
-@pytest.mark.parametrize("rows", [5, 20])
+@pytest.mark.parametrize("rows", [5, 7, 20, 4100])
 def test_fused_quant_equals_fused_then_quant(pkg, rows):
     """rlu_lru_fused_quant == r4d_lru_fused followed by rlu_quant_fp8_group(group 128), bit for
-    bit: cache state, both align outputs, e4m3 codes and scales."""
+    bit: cache state, both align outputs, e4m3 codes and scales; a row count that leaves a
+    quant workgroup part-used, and a prefill-sized chunk (8200 ids: the parallel placement)."""
     from importlib import import_module
     ops = import_module(pkg.__name__ + ".ops")
     ids_all, s = c1_trace()
