@@ -670,6 +670,13 @@ def main():
         ms1, _ = time_steps(torch, g1, ids1_dev, ids1_static, args.warmup, args.steps)
         out["b1_ms_per_step"] = round(ms1, 4)
         log(f"B=1 HBM-resident step: {ms1:.3f} ms")
+        r1 = gemm_roofline(torch, pkg, layers1, ids1[args.warmup + args.steps - 1], rows1)
+        out["b1_roofline"] = {k: r1[k] for k in ("bound", "achieved", "peak", "unit", "frac",
+                                                  "kernel", "avg_launch_us",
+                                                  "algorithmic_bytes_per_launch",
+                                                  "distinct_experts_per_layer")}
+        log(f"B=1 grouped GEMM: {out['b1_roofline']['achieved']} GB/s, frac "
+            f"{out['b1_roofline']['frac']}")
         del g1
         torch.cuda.synchronize()
         # the same B=1 steps with the miss gather (overlapped) in the graph

@@ -187,6 +187,17 @@ int rlu_moe_gemm_fp8blk_tiled(const void* qx, const float* xs, const void* wq, c
 int rlu_gemm_w4_m16(const void* x, int M, int K, const void* wq, const unsigned* sz, void* y,
                     int N, int wv, hipStream_t stream);
 
+/* Replaces the capture fn of tools/routecap/routecap.py:83-100 (five torch ops per layer
+ * there, one launch here; safe to record into a HIP graph). Copies one MoE layer's n routed
+ * expert ids (topk_ids, int32) into ring_ids[layer][slot][0..width) as int16, padded with -1.
+ * The layer-0 call of a step first advances *ctr and stores it in ring_step[slot];
+ * slot = *ctr % ring. ring_ids is [nlayer][ring][width] int16, ring_step [ring] int64
+ * (-1 = never written), ctr [1] int64 (0 at start). Returns -1 for n outside [0, width],
+ * layer outside [0, nlayer), ring <= 0 or a null buffer. */
+int rlu_route_capture(const int* topk_ids, int n, int layer, int nlayer, int ring, int width,
+                      short* ring_ids, long long* ring_step, long long* ctr,
+                      hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -11,6 +11,7 @@ from .lru import (LruCache, _align_sizes, _r4d_lru_fused, _r4d_lru_gather,  # no
                   _r4d_lru_manage)
 from . import ops  # noqa: F401
 from . import hot_profile  # noqa: F401
+from . import routecap  # noqa: F401
 from . import traces  # noqa: F401
 from . import w4  # noqa: F401
 from .moe import ExpertWeights, LruMoELayer  # noqa: F401

@@ -36,6 +36,7 @@ SIGNATURES: dict[str, tuple] = {
     "rlu_gemm_w4_m16": (_I, [_P, _I, _I, _P, _P, _P, _I, _I, _P]),
     "rlu_moe_gemm_tiles": (_I, [_P, _P, _I, _P, _P, _P]),
     "rlu_moe_gemm_fp8blk_tiled": (_I, [_P] * 8 + [_I, _P, _P] + [_I] * 5 + [_P]),
+    "rlu_route_capture": (_I, [_P] + [_I] * 5 + [_P] * 4),
 }
 
 

@@ -102,6 +102,9 @@ class LruMoELayer:
         self.eids_res = torch.empty_like(self.align[1])
         self.eids_new = torch.empty_like(self.align[1])
         self.ev_up = torch.cuda.Event()
+        # optional routing capture (routecap.RouteRing.fn(layer)), called with each step's
+        # topk_ids before the cache runs, as the router's capture_fn is
+        self.route_capture = None
         self.qx = torch.empty((self.M, self.H), dtype=ops.FP8, device=dev)
         self.xs = torch.empty((self.M, self.H // 128), dtype=torch.float32, device=dev)
         self.ic1 = torch.empty((self.mtk, self.N1), dtype=torch.bfloat16, device=dev)
@@ -211,6 +214,8 @@ class LruMoELayer:
         so the output is bit-identical."""
         M = hidden_states.shape[0]
         assert M == self.M and topk_ids.shape == (M, self.top_k)
+        if self.route_capture is not None:
+            self.route_capture(topk_ids)
         if overlap is None:
             overlap = self.cache.max_inserts > 0
         overlap = overlap and gather and side is not None

@@ -215,6 +215,10 @@ def test_layer_overlap_graph_replay(pkg, pool):
     out_a = torch.empty((M, H), dtype=torch.bfloat16, device=DEV)
     out_b = torch.empty_like(out_a)
     side = torch.cuda.Stream()
+    # the routing capture hook rides in the captured step too
+    from importlib import import_module
+    ring = import_module(pkg.__name__ + ".routecap").RouteRing(1, TOPK, DEV, ring=16, maxrows=M)
+    a.route_capture = ring.fn(0)
     # step 0 eager on both (loads every kernel), then capture the overlapped step
     gpu_case("overlap graph: eager step 0")
     ids0 = torch.from_numpy(ids_all[0]).to(DEV)
@@ -244,6 +248,13 @@ def test_layer_overlap_graph_replay(pkg, pool):
         out_a.zero_()                       # eager work between replays
         torch.cuda.synchronize()
     assert installs > 0, "the trace must install experts"
+    ring.poll()                             # steps 1..steps-1 finished; the last is the newest
+    got = ring.routes()
+    assert list(got["steps"]) == list(range(1, steps))
+    for t in range(steps - 1):
+        assert np.array_equal(got["ids"][t, 0], ids_all[t].reshape(-1).astype(np.int16))
+    assert np.array_equal(ring.ring_ids[0, steps % 16].cpu().numpy(),
+                          ids_all[steps - 1].reshape(-1).astype(np.int16))
     del g
 
 
