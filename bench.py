@@ -331,7 +331,7 @@ def lm_head_w4(torch, pkg, dev, Ms=(1, 4, 8), reps=20):
     return out
 
 
-def prefill_gemm(torch, pkg, dev, T=4096, reps=3):
+def prefill_gemm(torch, pkg, dev, T=4096, reps=3, lru=True):
     """The grouped GEMMs in the MFMA regime: a 4096-token prefill chunk, top-10 uniform over
     the 512 experts (seed 0), all experts HBM-resident (w13 / w2 fp8, fragment order), through
     the fused LRU + align (read-through: 512 distinct > 128) and the tiled kernel. Reports each
@@ -393,9 +393,11 @@ def prefill_gemm(torch, pkg, dev, T=4096, reps=3):
         b.record()
         torch.cuda.synchronize()
         return a.elapsed_time(b) * 1e3 / n
-    ua = timed_avg(lambda: cache.fused(ids_d, out=al))
-    uq = timed_avg(lambda: cache.fused_quant(ids_d, al, hs, qx, qs))
-    res = {"lru_align_us": round(ua, 1), "lru_align_quant_us": round(uq, 1)}
+    res = {}
+    if lru:
+        res["lru_align_us"] = round(timed_avg(lambda: cache.fused(ids_d, out=al)), 1)
+        res["lru_align_quant_us"] = round(timed_avg(lambda: cache.fused_quant(ids_d, al, hs, qx,
+                                                                              qs)), 1)
     for name, us, n, k in (("gate_up", u1, 2 * I, H), ("down", u2, H, I)):
         res[name] = dict(us=round(us, 1), tflops=round(2.0 * mtk * n * k / us / 1e6, 1),
                          weight_gbs=round(E * n * k / us / 1e3, 1))
@@ -462,6 +464,32 @@ def lru_insert_sweep(torch, pkg, dev, reps=50, rounds=5):
             row[str(k)] = round(times["full"] - times["restore"], 2)
         out[f"mk{mk}"] = row
     return out
+
+
+def counter_probe(torch, pkg, dev, calls=50):
+    """The workload of the LDS and MFMA counter runs: the fused LRU kernel in the insert storm
+    (E=512, S=257, mk 200 with no read-through; `calls` calls with 0 inserts, then `calls` with
+    64, each from the same pristine state, restored by copies between the calls), then the
+    prefill grouped GEMMs (gate_up and down, 4 launches each)."""
+    for k in (0, 64):
+        rng = np.random.default_rng(100 + k)
+        hot = np.sort(rng.choice(E, S, replace=False))
+        rank = {int(e): i for i, e in enumerate(rng.permutation(hot))}
+        cache = pkg.LruCache.build(E, hot, rank, dev)
+        cache.max_distinct = E
+        ids = torch.from_numpy(pkg.traces.insert_storm_ids(rng, hot, E, 200, k)).to(dev)
+        align = cache.alloc_align(200)
+        pristine = [t.clone() for t in cache.state()]
+        for _ in range(calls):
+            for t, v in zip(cache.state(), pristine):
+                t.copy_(v)
+            cache.fused(ids, out=align)
+        torch.cuda.synchronize()
+        assert int(cache.n_miss.item()) == k
+    res = prefill_gemm(torch, pkg, dev, reps=3, lru=False)
+    print(json.dumps({"counter_probe": f"lru_k: {calls} calls at 0 inserts, then {calls} at 64 "
+                                       "(mk 200); then tiled_k gate_up x4, down x4 (4096 "
+                                       "tokens)", "prefill": res}), flush=True)
 
 
 # ---- CPU baseline: the oracle restatement of one layer step, timed on the host ------------------
@@ -531,6 +559,9 @@ def main():
     ap.add_argument("--only-b4", action="store_true",
                     help="only the B=4 HBM-resident step (the profiled command)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--counter-probe", action="store_true",
+                    help="for LDS / MFMA counter runs: the fused LRU kernel in the insert storm "
+                         "and the prefill grouped GEMMs, then exit")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="for counter runs: one eager B=4 step of the 52 layers, their 104 "
                          "grouped-GEMM launches once more, then a 256 MiB device copy (the "
@@ -549,6 +580,9 @@ def main():
     pkg.lib()                                   # fail loudly without the HIP library
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.counter_probe:
+        counter_probe(torch, pkg, dev)
+        return
     t_setup = time.perf_counter()
     log("generating 512 fp8 experts")
     pool = make_pool(torch, dev, pkg.ops)
