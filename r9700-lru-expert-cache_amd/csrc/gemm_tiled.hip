@@ -10,8 +10,8 @@
 //                  the 16 weight strips (fragment order, 2 KB contiguous each) in LDS, double-
 //                  buffered with one barrier per step; wave w runs the MFMAs of blocks
 //                  w % 2, w % 2 + 2, ... (interleaved, so a short tile still splits evenly) and
-//                  strips 4 (w / 2) .. 4 (w / 2) + 3. The expert's weights stream from HBM once per tile instead
-//                  of once per 16-row block. Accumulation is acc += mfma * (xs * ws) per step,
+//                  strips 4 (w / 2) .. 4 (w / 2) + 3. The expert's weights stream from HBM
+//                  once per tile instead of once per 16-row block. Accumulation is acc += mfma * (xs * ws) per step,
 //                  as in moe_gemm_k, so both kernels give the same sums up to the association of
 //                  the (shared) per-step products -- each output is the same sequence of fma's.
 #include <hip/hip_runtime.h>

@@ -6,11 +6,11 @@
 // The implementation is this build's own, shaped for wave64 CDNA4:
 //
 //  * One workgroup of 256 threads (one wave per SIMD), seven barriers for the fused kernel at
-//    decode sizes (three for the manager). Every global load is issued up front, so the kernel pays one
-//    memory round trip, not one per phase. Decode-sized align outputs are built in LDS and
-//    written once, coalesced, with the sentinels past num_post_pad written directly; larger
-//    ones are pre-filled with their sentinels in global memory, and only the first barrier
-//    waits for global stores (the rest order LDS only).
+//    decode sizes (three for the manager). Every global load is issued up front, so the kernel
+//    pays one memory round trip, not one per phase. Decode-sized align outputs are built in
+//    LDS and written once, coalesced, with the sentinels past num_post_pad written directly;
+//    larger ones are pre-filled with their sentinels in global memory, and only the first
+//    barrier waits for global stores (the rest order LDS only).
 //  * Cross-lane reductions and scans are DPP + v_readlane (wave-uniform scalars), not LDS
 //    shuffles.
 //  * Routed / non-resident sets are 64-bit-word bitmaps built from wave ballots; misses are

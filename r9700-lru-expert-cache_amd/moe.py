@@ -68,10 +68,12 @@ class LruMoELayer:
         """npw / sk: 16-column tiles per item and K split of gate_up (1) and down (2); the
         defaults are the fastest measured at the decode shapes (hidden 2560, intermediate
         768): gate_up splits K over 2 waves above 8 tokens (20 tokens: 3.70 vs 3.95 ms per
-        52-layer step) and not at all up to 8 (5 tokens: 3.007 vs 3.038 ms). max_inserts: cap on cache inserts per step (default
-        VLLM_R4D_LRU_MAX_INSERTS, 64); 0 is the static hot/cold arm -- the warm-start set stays
-        resident and every other routed expert is read from the full tensor
-        (r4d_mxfp4_moe.py.static.diff, and the README's MAX_INSERTS=0 ablation)."""
+        52-layer step) and not at all up to 8 (5 tokens: 3.007 vs 3.038 ms).
+
+        max_inserts: cap on cache inserts per step (default VLLM_R4D_LRU_MAX_INSERTS, 64); 0 is
+        the static hot/cold arm -- the warm-start set stays resident and every other routed
+        expert is read from the full tensor (r4d_mxfp4_moe.py.static.diff, and the README's
+        MAX_INSERTS=0 ablation)."""
         dev = torch.device(device)
         self.full = full
         self.full_ptrs = full.ptrs()
