@@ -509,32 +509,79 @@ def cpu_baseline(pool_cpu_w13, pool_cpu_w2, ids, budget_s=10.0):
     done = 0
     t0 = time.perf_counter()
     per = []
+    pieces = {k: [] for k in ("lru_fused_align", "group_quant", "gate_up", "silu_mul_quant",
+                              "down", "moe_sum")}
+
+    def timed(name, fn):
+        a = time.perf_counter()
+        r = fn()
+        pieces[name].append(1e3 * (time.perf_counter() - a))
+        return r
     while time.perf_counter() - t0 < budget_s and done < LAYERS:
         l = done
         _, perm0 = layer_trace(l, rows, 1)
         hot, rank = trace.warm_hot(perm0, S)
         st = olru.warm_start(E, S, hot, rank)
         tl = time.perf_counter()
-        al = olru.fused(st, ids[0, l].reshape(-1), 16)
-        qx, xs = fp8.group_quant(x, 128)
+        timed("lru_fused_align", lambda: olru.fused(st, ids[0, l].reshape(-1), 16))
+        qx, xs = timed("group_quant", lambda: fp8.group_quant(x, 128))
         used = np.unique(ids[0, l])
         W13 = {int(e): pool_cpu_w13[int(e)] for e in used}
         W2 = {int(e): pool_cpu_w2[int(e)] for e in used}
         table = np.arange(E, dtype=np.int32)
         a_all = olru.align(ids[0, l].reshape(-1), E, E, table, 16, *olru.align_sizes(mtk, E, 16))
-        y1 = ogemm.moe_gemm(qx, xs, _Dict(W13, 0), _Dict(W13, 1), *a_all[:3], mtk, TOPK)
-        _, q2, s2 = fp8.silu_mul_quant(fp8.bf16_round(y1.astype(np.float32)), 128)
-        y2 = ogemm.moe_gemm(q2, s2, _Dict(W2, 0), _Dict(W2, 1), *a_all[:3], mtk, 1, tw=tw)
-        ogemm.moe_sum(fp8.bf16_round(y2.astype(np.float32)), rows, TOPK)
+        y1 = timed("gate_up", lambda: ogemm.moe_gemm(qx, xs, _Dict(W13, 0), _Dict(W13, 1),
+                                                     *a_all[:3], mtk, TOPK))
+        _, q2, s2 = timed("silu_mul_quant",
+                          lambda: fp8.silu_mul_quant(fp8.bf16_round(y1.astype(np.float32)), 128))
+        y2 = timed("down", lambda: ogemm.moe_gemm(q2, s2, _Dict(W2, 0), _Dict(W2, 1),
+                                                  *a_all[:3], mtk, 1, tw=tw))
+        timed("moe_sum", lambda: ogemm.moe_sum(fp8.bf16_round(y2.astype(np.float32)), rows,
+                                               TOPK))
         per.append(time.perf_counter() - tl)
         done += 1
     ms_layer = 1e3 * float(np.median(per))
+    # the two lm_head GEMVs through the oracle on a 2048-row slice of the vocab (median of 3),
+    # scaled to the 151936 rows (the oracle is linear in the rows)
+    from oracle import w4 as ow4
+    vocab, nsl = 151936, 2048
+
+    def med3(fn):
+        ts = []
+        for _ in range(3):
+            a = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - a)
+        return float(np.median(ts))
+    g = np.random.default_rng(5)
+    wsl = (g.standard_normal((nsl, H)) * 0.02).astype(np.float32)
+    xq5, xs5 = fp8.group_quant(fp8.bf16_round(g.standard_normal((5, H)).astype(np.float32)), 128)
+    wq, wsc = fp8.block_quant_weight(wsl)
+    head_fp8 = 1e3 * med3(lambda: ogemm.dense(xq5, xs5, wq, wsc)) * vocab / nsl
+    q4, sc4, z4 = ow4.quantize_w4(wsl)
+    x1 = fp8.bf16_round(g.standard_normal((1, H)).astype(np.float32))
+    head_w4 = 1e3 * med3(lambda: ow4.gemv(x1, q4, sc4, z4)) * vocab / nsl
     return dict(value=round(ms_layer * LAYERS, 1), unit="ms/step", cores=int(threads),
                 kind="port",
                 sample=f"{done} of the 52 layers of one B={rows // 5} step through the numpy "
                        f"oracle (fused LRU + align, group quant, fp32-dequant GEMMs in float64, "
                        f"SiLU-quant, moe_sum); median layer time x 52",
-                cpu=platform.processor() or platform.machine(), os_cpu_count=os.cpu_count())
+                pieces_ms_per_layer={k: round(float(np.median(v)), 3)
+                                     for k, v in pieces.items()},
+                lm_head_ms={"fp8_M5": round(head_fp8, 1), "w4_M1": round(head_w4, 1),
+                            "sample": f"{nsl} of the {vocab} vocab rows, scaled"},
+                cpu=_cpu_model(), os_cpu_count=os.cpu_count())
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
 
 class _Dict:
