@@ -242,6 +242,8 @@ PLACE_CASES = [
     ("L-past-the-blocks", 9000, 16, 9000 + 512 * 15, 100, 0.0),
     ("runtime-bs-64", 5000, 64, None, None, 0.02),
     ("ids-not-16-byte-aligned", 7003, 16, None, None, 0.01),
+    ("ids-not-16-byte-aligned-single-workgroup", 1001, 16, None, None, 0.01),
+    ("single-workgroup-vector-count", 1500, 16, None, None, 0.02),
 ]
 
 
