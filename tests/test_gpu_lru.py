@@ -186,6 +186,34 @@ def test_victim_cases_vs_reference_kernel(mine, ref, case):
                 _cmp_align_multiset(oa[3:6], ob[3:6], ids.size)
 
 
+@pytest.mark.parametrize("rows", [40, 205])
+def test_chunked_sizes_vs_reference_kernel(mine, ref, rows):
+    """tests/lru/test_fused.py:265-280's largest sizes (mk 400 and 2050) through both kernels
+    from the same state, 3 steps with inserts: state bit-exact, buckets equal as multisets
+    (the reference places above 256 ids with atomic cursors). At mk 2050 this library ranks
+    the ids in its many-workgroup placement kernel."""
+    E, S = 512, 257
+    rng = np.random.default_rng(rows)
+    _, s = victim_case(E=E, S=S, mk=10, k_cold=0, maxi=64, seed=9)
+    s.max_distinct = E
+    a, b = to_dev(s), to_dev(s)
+    for n in range(3):
+        pool = rng.choice(E, 350, replace=False)
+        ids = np.concatenate([rng.choice(pool, 10, replace=False)
+                              for _ in range(rows)]).astype(np.int32)
+        ids_t = torch.from_numpy(ids).to(DEV)
+        oa, ob = new_out(ids.size, E, fill=-12345), new_out(ids.size, E, fill=-12345)
+        gpu_case(f"vs-ref chunked rows={rows} step {n}")
+        call(mine, "fused", ids_t, a, s.max_distinct, s.max_inserts, oa)
+        call(ref, "fused", ids_t, b, s.max_distinct, s.max_inserts, ob)
+        torch.cuda.synchronize()
+        for nm in NAMES:
+            assert torch.equal(a[nm], b[nm]), f"rows={rows} step {n}: '{nm}'"
+        assert int(a["n_miss"].item()) > 0
+        _cmp_align_multiset(oa[0:3], ob[0:3], ids.size)
+        _cmp_align_multiset(oa[3:6], ob[3:6], ids.size)
+
+
 def test_c1_trace_vs_reference_kernel(mine, ref):
     """The 64-step trace through both kernels, side by side: identical state every step."""
     ids_all, s = c1_trace()
