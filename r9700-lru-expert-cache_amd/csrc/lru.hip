@@ -24,8 +24,8 @@
 //  * Align is stable at every mk: a token's rank inside its bucket is the number of earlier
 //    tokens routed to the same expert -- up to 256 tokens a popcount of the expert's token
 //    bitmap below it (each token places itself), above that a bit-sliced wave match plus
-//    per-wave counts in LDS. Above 2048 tokens the ranking moves to place_k, one workgroup per
-//    1024 tokens, each counting the tokens before its own.
+//    per-wave counts in LDS. Above 2048 tokens the sorted arrays are written by place_k, one
+//    1024-thread workgroup per 1024 tokens, each counting the tokens before its own.
 //
 // Preconditions (checked by the reference's own tests after every step, tests/lru/test_lru.py:
 // 138-145): table/map_cold complementary, table[slot_expert[s]] == s for resident slots,
@@ -485,7 +485,9 @@ __global__ __launch_bounds__(NT) void lru_k(
       }
     } else {
       reinterpret_cast<uint4*>(&L.tk.wcnt[0][0])[t] = make_uint4(0, 0, 0, 0);
-      fill_align(sorted_hot, sorted_cold, eids_hot, eids_cold, Lsz, NB, mk, vec_out);
+      // deferred placement: place_k writes all of the sorted arrays, sentinels included
+      fill_align(sorted_hot, sorted_cold, eids_hot, eids_cold, defer_place ? 0 : Lsz, NB, mk,
+                 vec_out);
     }
     for (int i = t; i < S; i += NT) L.cnt_h[i] = 0;
   }
@@ -864,63 +866,72 @@ __global__ __launch_bounds__(NT) void split_fresh_k(const int* __restrict__ eids
 }
 
 // ---- placement for large token counts, many workgroups ----------------------------------
-// Above PLACE_MIN tokens the fused launch stops once the sentinels, the bucket counts, starts,
-// expert ids and num_post_pad are written; place_k then ranks the tokens. Workgroup c takes
-// tokens [c PC, (c + 1) PC): it counts the earlier tokens per expert with LDS atomics (order
-// does not matter for a count), then ranks its own tokens NT at a time in index order, as the
-// single-workgroup loop does, so every bucket still lists its tokens in ascending index order.
+// Above PLACE_MIN tokens the fused launch stops once the expert-id sentinels, the bucket
+// counts, starts, expert ids and num_post_pad are written; place_k writes everything of the
+// sorted arrays. Workgroup c (PT threads) takes tokens [c PT, (c + 1) PT):
+//  * it counts every id per expert, and separately those before its own tokens (LDS atomics;
+//    order does not matter for a count);
+//  * it ranks its own tokens in index order (bit-sliced wave match + per-wave counts), as the
+//    single-workgroup loop does, so every bucket lists its tokens in ascending index order;
+//  * it writes the padding sentinels of its share of the experts' buckets, [start + count,
+//    start + padded count), and its share of [num_post_pad, L).
+// Token positions, padding and the tail are disjoint, so no two workgroups write one entry.
 // A routed expert's bucket is its slot in the updated table (hot) or itself (cold); a bucket
 // starts at the first block of its run in eids_hot / eids_cold. The host takes this route only
 // when NB * bs >= L: then every bucket that starts below L has its first block recorded, and
-// the others (start left at L) place nothing.
-constexpr int PC = 1024;            // tokens ranked by one placement workgroup
+// the others (start left at L) write nothing.
+constexpr int PT = 1024;            // threads and tokens of one placement workgroup
+constexpr int PWV = PT / WAVE;
 constexpr int PLACE_MIN = 2048;     // the fused launch defers placement above this many tokens
-constexpr int PLOADS = 16;          // id loads in flight per thread while counting (unaligned)
-constexpr int PB = 8;               // expert-id blocks per thread in flight
+constexpr int PLOADS = 8;           // id loads in flight per thread while counting (unaligned)
+constexpr int PB = 4;               // expert-id blocks per thread in flight
 
 struct PlaceLds {
   int start_h[MAXS];
   int start_c[MAXE];
-  int cnt[MAXE];                    // tokens of the expert before the NT tokens being ranked
+  int before[MAXE];                 // tokens of the expert before this workgroup's
+  int total[MAXE];                  // tokens of the expert in the step
   int tab[MAXE];                    // updated table
-  alignas(16) uint8_t wcnt[NW][MAXE];  // tokens of the expert per wave among those NT tokens
+  alignas(16) uint8_t wcnt[PWV][MAXE];  // tokens of the expert per wave among this chunk
 };
 
-__global__ __launch_bounds__(NT) void place_k(const int* __restrict__ ids, int mk, int E, int S,
+__device__ __forceinline__ void count2(PlaceLds& P, int e, int i, int c0, int E) {
+  if ((unsigned)e < (unsigned)E) {
+    atomicAdd(&P.total[e], 1);
+    if (i < c0) atomicAdd(&P.before[e], 1);
+  }
+}
+
+__global__ __launch_bounds__(PT) void place_k(const int* __restrict__ ids, int mk, int E, int S,
                                               const int* __restrict__ table,
                                               const int* __restrict__ eids_hot,
-                                              const int* __restrict__ eids_cold, int NB, int bs,
+                                              const int* __restrict__ eids_cold,
+                                              const int* __restrict__ npad_hot,
+                                              const int* __restrict__ npad_cold, int NB, int bs,
                                               int Lsz, int* __restrict__ sorted_hot,
                                               int* __restrict__ sorted_cold) {
   __shared__ PlaceLds P;
   const int t = threadIdx.x, w = t / WAVE;
-  const int c0 = blockIdx.x * PC, c1 = min(c0 + PC, mk);
-  // this workgroup's ids and the table first: nothing below waits on a load it does not need
-  constexpr int PU = PC / NT;
-  int own[PU];
-#pragma unroll
-  for (int u = 0; u < PU; ++u) own[u] = ids[min(c0 + t + u * NT, c1 - 1)];
-  int tb[EJ];
-#pragma unroll
-  for (int j = 0; j < EJ; ++j) tb[j] = table[min(t + NT * j, E - 1)];
-  for (int k = t; k < S; k += NT) P.start_h[k] = Lsz;
-#pragma unroll
-  for (int j = 0; j < EJ; ++j) {
-    const int e = t + NT * j;
-    if (e < E) {
-      P.start_c[e] = Lsz;
-      P.cnt[e] = 0;
-      P.tab[e] = tb[j];
-    }
+  const int c0 = blockIdx.x * PT, c1 = min(c0 + PT, mk);
+  // this workgroup's id and the table first: nothing below waits on a load it does not need
+  const int own = ids[min(c0 + t, c1 - 1)];
+  const int tb = table[min(t, E - 1)];              // E <= MAXE == PT
+  const int nph = npad_hot[0], npc = npad_cold[0];
+  if (t < S) P.start_h[t] = Lsz;
+  if (t < E) {
+    P.start_c[t] = Lsz;
+    P.before[t] = 0;
+    P.total[t] = 0;
+    P.tab[t] = tb;
   }
-  reinterpret_cast<uint4*>(&P.wcnt[0][0])[t] = make_uint4(0, 0, 0, 0);   // NW * MAXE bytes
+  reinterpret_cast<uint4*>(&P.wcnt[0][0])[t] = make_uint4(0, 0, 0, 0);   // PWV * MAXE bytes
   lds_barrier();
   // the first block of each bucket's run; PB blocks per thread in flight
-  for (int b0 = 0; b0 < NB; b0 += PB * NT) {
+  for (int b0 = 0; b0 < NB; b0 += PB * PT) {
     int eh[PB], ec[PB], ph[PB], pc[PB];
 #pragma unroll
     for (int u = 0; u < PB; ++u) {
-      const int b = min(b0 + t + u * NT, NB - 1), bp = max(b - 1, 0);
+      const int b = min(b0 + t + u * PT, NB - 1), bp = max(b - 1, 0);
       eh[u] = eids_hot[b];
       ec[u] = eids_cold[b];
       ph[u] = eids_hot[bp];
@@ -928,56 +939,85 @@ __global__ __launch_bounds__(NT) void place_k(const int* __restrict__ ids, int m
     }
 #pragma unroll
     for (int u = 0; u < PB; ++u) {
-      const int b = b0 + t + u * NT;
+      const int b = b0 + t + u * PT;
       if (b < NB) {
         if ((unsigned)eh[u] < (unsigned)S && (b == 0 || eh[u] != ph[u])) P.start_h[eh[u]] = b * bs;
         if ((unsigned)ec[u] < (unsigned)E && (b == 0 || ec[u] != pc[u])) P.start_c[ec[u]] = b * bs;
       }
     }
   }
-  // the tokens before this workgroup's, per expert
-  const bool vec = (((uintptr_t)ids & 15) == 0);
-  if (vec) count_ids_vec(ids, 0, c0, E, P.cnt);     // c0 is a multiple of 4
-  for (int i = t; !vec && i < c0; i += PLOADS * NT) {
-    int e[PLOADS];
+  // every id, per expert: VL 16-byte loads in flight per thread when ids is 16-byte aligned
+  if ((((uintptr_t)ids & 15) == 0)) {
+    const int4* v = reinterpret_cast<const int4*>(ids);
+    const int nv = mk / 4;
+    for (int j = t; j < nv; j += VL * PT) {
+      int4 x[VL];
 #pragma unroll
-    for (int u = 0; u < PLOADS; ++u) e[u] = ids[min(i + u * NT, c0 - 1)];
+      for (int u = 0; u < VL; ++u) x[u] = v[min(j + u * PT, nv - 1)];
 #pragma unroll
-    for (int u = 0; u < PLOADS; ++u)
-      if (i + u * NT < c0 && (unsigned)e[u] < (unsigned)E) atomicAdd(&P.cnt[e[u]], 1);
-  }
-  lds_barrier();
-  const int kbits = E > 1 ? 32 - __clz(E - 1) : 0;
-#pragma unroll
-  for (int u = 0; u < PU; ++u) {
-    if (c0 + u * NT >= c1) break;                   // uniform over the workgroup
-    const int i = c0 + u * NT + t;
-    const int e = i < c1 ? own[u] : -1;
-    const bool v = (unsigned)e < (unsigned)E;
-    const uint64_t m = match_any(e, v, kbits);
-    const int inrank = mbcnt(m);
-    if (v && inrank == 0) P.wcnt[w][e] = (uint8_t)__popcll(m);
-    lds_barrier();
-    if (v) {
-      int rank = P.cnt[e] + inrank;
-      for (int ww = 0; ww < w; ++ww) rank += P.wcnt[ww][e];
-      const int s = P.tab[e];
-      const bool hot = (unsigned)s < (unsigned)S;
-      const int pos = (hot ? P.start_h[s] : P.start_c[e]) + rank;
-      if (pos < Lsz) {
-        if (hot)
-          sorted_hot[pos] = i;
-        else
-          sorted_cold[pos] = i;
+      for (int u = 0; u < VL; ++u) {
+        const int q = j + u * PT;
+        if (q < nv) {
+          count2(P, x[u].x, 4 * q, c0, E);
+          count2(P, x[u].y, 4 * q + 1, c0, E);
+          count2(P, x[u].z, 4 * q + 2, c0, E);
+          count2(P, x[u].w, 4 * q + 3, c0, E);
+        }
       }
     }
-    lds_barrier();
-    if (v && inrank == 0) {                         // fold this wave's count, clear its entry
-      atomicAdd(&P.cnt[e], __popcll(m));
-      P.wcnt[w][e] = 0;
+    if (t < mk - 4 * nv) count2(P, ids[4 * nv + t], 4 * nv + t, c0, E);
+  } else {
+    for (int i = t; i < mk; i += PLOADS * PT) {
+      int x[PLOADS];
+#pragma unroll
+      for (int u = 0; u < PLOADS; ++u) x[u] = ids[min(i + u * PT, mk - 1)];
+#pragma unroll
+      for (int u = 0; u < PLOADS; ++u)
+        if (i + u * PT < mk) count2(P, x[u], i + u * PT, c0, E);
     }
-    lds_barrier();
   }
+  lds_barrier();
+  // this workgroup's tokens, in index order
+  const int kbits = E > 1 ? 32 - __clz(E - 1) : 0;
+  const int i = c0 + t;
+  const int e = i < c1 ? own : -1;
+  const bool v = (unsigned)e < (unsigned)E;
+  const uint64_t m = match_any(e, v, kbits);
+  const int inrank = mbcnt(m);
+  if (v && inrank == 0) P.wcnt[w][e] = (uint8_t)__popcll(m);
+  lds_barrier();
+  if (v) {
+    int rank = P.before[e] + inrank;
+    for (int ww = 0; ww < w; ++ww) rank += P.wcnt[ww][e];
+    const int sl = P.tab[e];
+    const bool hot = (unsigned)sl < (unsigned)S;
+    const int pos = (hot ? P.start_h[sl] : P.start_c[e]) + rank;
+    if (pos < Lsz) {
+      if (hot)
+        sorted_hot[pos] = i;
+      else
+        sorted_cold[pos] = i;
+    }
+  }
+  // padding of this workgroup's experts (one per thread), then its share of the tails
+  const int ex = blockIdx.x + gridDim.x * t;
+  if (ex < E) {
+    const int cnt = P.total[ex];
+    if (cnt > 0) {
+      const int sl = P.tab[ex];
+      const bool hot = (unsigned)sl < (unsigned)S;
+      const int st = hot ? P.start_h[sl] : P.start_c[ex];
+      const int end = min(st + (cnt + bs - 1) / bs * bs, Lsz);
+      for (int p = st + cnt; p < end; ++p) {
+        if (hot)
+          sorted_hot[p] = mk;
+        else
+          sorted_cold[p] = mk;
+      }
+    }
+  }
+  for (int p = max(nph, 0) + blockIdx.x * PT + t; p < Lsz; p += gridDim.x * PT) sorted_hot[p] = mk;
+  for (int p = max(npc, 0) + blockIdx.x * PT + t; p < Lsz; p += gridDim.x * PT) sorted_cold[p] = mk;
 }
 
 // Placement moves to place_k for large token counts when every bucket start below L is
@@ -987,10 +1027,12 @@ static inline bool defer_placement(int mk, int bs, int L, int NB) {
 }
 
 static inline void launch_place(const int* ids, int mk, int E, int S, const int* table,
-                                const int* eids_hot, const int* eids_cold, int NB, int bs, int L,
-                                int* sorted_hot, int* sorted_cold, hipStream_t stream) {
-  hipLaunchKernelGGL(place_k, dim3((mk + PC - 1) / PC), dim3(NT), 0, stream, ids, mk, E, S,
-                     table, eids_hot, eids_cold, NB, bs, L, sorted_hot, sorted_cold);
+                                const int* eids_hot, const int* eids_cold, const int* npad_hot,
+                                const int* npad_cold, int NB, int bs, int L, int* sorted_hot,
+                                int* sorted_cold, hipStream_t stream) {
+  hipLaunchKernelGGL(place_k, dim3((mk + PT - 1) / PT), dim3(PT), 0, stream, ids, mk, E, S,
+                     table, eids_hot, eids_cold, npad_hot, npad_cold, NB, bs, L, sorted_hot,
+                     sorted_cold);
 }
 
 }  // namespace rlu
@@ -1028,8 +1070,8 @@ int r4d_lru_fused(const int* topk_ids, int mk, int E, int S, int max_distinct,
                      n_miss, bs, L, NB, sorted_hot, eids_hot, npad_hot, sorted_cold, eids_cold,
                      npad_cold, rlu::QuantJob{}, rlu::aligned16(sorted_hot, sorted_cold), defer);
   if (defer)
-    rlu::launch_place(topk_ids, mk, E, S, table, eids_hot, eids_cold, NB, bs, L, sorted_hot,
-                      sorted_cold, stream);
+    rlu::launch_place(topk_ids, mk, E, S, table, eids_hot, eids_cold, npad_hot, npad_cold, NB,
+                      bs, L, sorted_hot, sorted_cold, stream);
   return (int)hipGetLastError();
 }
 
@@ -1058,8 +1100,8 @@ int rlu_lru_fused_quant(const int* topk_ids, int mk, int E, int S, int max_disti
                      rlu::QuantJob{(const uint16_t*)x, rows, K, ldx, (uint8_t*)q, scale},
                      rlu::aligned16(sorted_hot, sorted_cold), defer);
   if (defer)
-    rlu::launch_place(topk_ids, mk, E, S, table, eids_hot, eids_cold, NB, bs, L, sorted_hot,
-                      sorted_cold, stream);
+    rlu::launch_place(topk_ids, mk, E, S, table, eids_hot, eids_cold, npad_hot, npad_cold, NB,
+                      bs, L, sorted_hot, sorted_cold, stream);
   return (int)hipGetLastError();
 }
 
