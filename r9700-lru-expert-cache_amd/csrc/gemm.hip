@@ -67,16 +67,37 @@ __global__ __launch_bounds__(GWV * WAVE) void moe_gemm_k(
     const uint8_t* __restrict__ wq = second ? s1.wq : s0.wq;
     const float* __restrict__ ws = second ? s1.ws : s0.ws;
     const int* __restrict__ sids = second ? s1.sorted_ids : s0.sorted_ids;
+    // the block's expert id and its 16 row ids in one round trip (b is 0 for a dead item, and
+    // every sorted-id array holds at least one block): this lane's A row (operand layout) and
+    // the four output rows it holds (D layout: rows 4 c4 + i, column r16)
+    int so = DENSE ? r16 : mtk;
+    int sod[4] = {mtk, mtk, mtk, mtk};
+    if (!DENSE) {
+      int ids[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) ids[i] = sids[b * 16 + i];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) so = r16 == i ? ids[i] : so;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        int v = ids[i];
+#pragma unroll
+        for (int c = 1; c < 4; ++c) v = (lane >> 4) == c ? ids[4 * c + i] : v;
+        sod[i] = v;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sod[i] = 4 * (lane >> 4) + i;
+    }
     const int eid = (DENSE || !live) ? 0 : (second ? s1.expert_ids : s0.expert_ids)[b];
     live = live && eid >= 0;
     v4f acc[NPW];
 #pragma unroll
     for (int s = 0; s < NPW; ++s) acc[s] = v4f{0.f, 0.f, 0.f, 0.f};
-    int sod[4] = {mtk, mtk, mtk, mtk};
     float twv[4] = {1.f, 1.f, 1.f, 1.f};
     if (live)
-      item_mma<NPW, SKW, DENSE>(qx, xs, wq, ws, sids, eid, b, n0, tw, mtk, top_k, K, N, ks, sx,
-                                acc, sod, twv);
+      item_mma<NPW, SKW, DENSE>(qx, xs, wq, ws, so, eid, n0, tw, mtk, top_k, K, N, ks, sx, acc,
+                                sod, twv);
     if (SKW > 1)
       splitk_reduce<NPW, SKW>(acc, red + (size_t)parity * GWV * NPW * 4 * WAVE, wv, ks);
     if (live && ks == 0) {

@@ -32,13 +32,15 @@ __host__ __device__ __forceinline__ int item_steps(int K) {
 // Accumulates this wave's K share of the item into acc (D layout: lane l holds rows
 // 4 (l / 16) + i, column l % 16 of each strip) and returns the item's row ids for those rows
 // (sod; mtk = padding) and, for wave ks == 0 when tw is given, their routed weights (twv).
+// so / sod: this lane's A row and its four output rows, which the caller takes from the
+// block's 16 sorted ids, loaded together with the expert id.
 // sx: this wave's item_steps() x 16 floats of LDS. D: register ring depth.
 template <int NPW, int SKW, bool DENSE, int D = ring_of(NPW)>
 __device__ __forceinline__ void item_mma(const uint8_t* __restrict__ qx,
                                          const float* __restrict__ xs,
                                          const uint8_t* __restrict__ wq,
                                          const float* __restrict__ ws,
-                                         const int* __restrict__ sids, int eid, int b, int n0,
+                                         int so, int eid, int n0,
                                          const float* __restrict__ tw, int mtk, int top_k, int K,
                                          int N, int ks, float* sx, v4f (&acc)[NPW],
                                          int (&sod)[4], float (&twv)[4]) {
@@ -47,26 +49,6 @@ __device__ __forceinline__ void item_mma(const uint8_t* __restrict__ qx,
   const int nkg = K / 128;
   const int kpw = nkg / SKW;
   const int nsteps = item_steps<NPW, SKW, D>(K);
-  // the block's 16 row ids (scalar loads), this lane's A row (operand layout) and the four
-  // output rows it holds (D layout: rows 4 c4 + i, column r16)
-  int so = DENSE ? r16 : mtk;
-  if (!DENSE) {
-    int ids[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) ids[i] = sids[b * 16 + i];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) so = r16 == i ? ids[i] : so;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      int v = ids[i];
-#pragma unroll
-      for (int c = 1; c < 4; ++c) v = c4 == c ? ids[4 * c + i] : v;
-      sod[i] = v;
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) sod[i] = 4 * c4 + i;
-  }
   if (tw && ks == 0) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) twv[i] = tw[sod[i] < mtk ? sod[i] : 0];
