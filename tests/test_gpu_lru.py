@@ -312,6 +312,49 @@ def test_fused_parallel_placement(mine, case):
             assert np.array_equal(g.cpu().numpy(), w), f"{tag} step {n}: output {i}"
 
 
+def test_fused_prefill_size_graph_replay(mine):
+    """A prefill-sized fused call (8200 ids: two launches, the second ranking the ids) captured
+    once as a HIP graph and replayed with new routing: each replay's state and outputs equal an
+    eager call on a twin state, with eager work and synchronizations between replays."""
+    E, S, mk = 512, 257, 8200
+    rng = np.random.default_rng(21)
+    _, s = victim_case(E=E, S=S, mk=10, k_cold=0, maxi=64, seed=13)
+    s.max_distinct = E
+    a, b = to_dev(s), to_dev(s)
+    ids_st = torch.zeros(mk, dtype=torch.int32, device=DEV)
+    oa, ob = new_out(mk, E), new_out(mk, E)
+    first = torch.from_numpy(rng.choice(rng.choice(E, 350, replace=False), mk)
+                             .astype(np.int32)).to(DEV)
+    ids_st.copy_(first)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):                   # step 0 eager on both, off the capture
+        call(mine, "fused", ids_st, a, s.max_distinct, s.max_inserts, oa)
+        call(mine, "fused", first, b, s.max_distinct, s.max_inserts, ob)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        call(mine, "fused", ids_st, a, s.max_distinct, s.max_inserts, oa)
+    for n in range(3):
+        ids = torch.from_numpy(rng.choice(rng.choice(E, 350, replace=False), mk)
+                               .astype(np.int32)).to(DEV)
+        ids_st.copy_(ids)
+        gpu_case(f"prefill-size graph replay {n}")
+        g.replay()
+        call(mine, "fused", ids, b, s.max_distinct, s.max_inserts, ob)
+        torch.cuda.synchronize()
+        for nm in NAMES:
+            assert torch.equal(a[nm], b[nm]), f"replay {n}: '{nm}'"
+        for i in range(6):
+            assert torch.equal(oa[i], ob[i]), f"replay {n}: align output {i}"
+        assert int(a["n_miss"].item()) > 0
+        for o in oa:                                # eager work between replays
+            o.fill_(-7)
+        torch.cuda.synchronize()
+    del g
+
+
 def test_fused_edges(mine):
     """tests/lru/test_fused.py:282-293: forced read-through and a zero-miss replay."""
     ids_all, s = c1_trace()
