@@ -24,7 +24,7 @@
 //  * Align is stable at every mk: a token's rank inside its bucket is the number of earlier
 //    tokens routed to the same expert -- up to 256 tokens a popcount of the expert's token
 //    bitmap below it (each token places itself), above that a bit-sliced wave match plus
-//    per-wave counts in LDS. Above 2048 tokens the sorted arrays are written by place_k, one
+//    per-wave counts in LDS. Above 1536 tokens the sorted arrays are written by place_k, one
 //    1024-thread workgroup per 1024 tokens, each counting the tokens before its own.
 //
 // Preconditions (checked by the reference's own tests after every step, tests/lru/test_lru.py:
@@ -755,11 +755,16 @@ __global__ __launch_bounds__(NT) void lru_k(
   if (defer_place) return;                        // place_k ranks the tokens in parallel
 
   // ---- general placement, chunk by chunk of NT tokens in index order ---------------------
+  // the next chunk's id is loaded one chunk ahead, so no chunk waits for a memory round trip
+  int nxt = NT + t < mk ? ids[NT + t] : -1;
   for (int c = 0; c * NT < mk; ++c) {
     const int i = c * NT + t;
     int e = tok0;
     bool v = v0;
     if (c > 0) {
+      const int cur = nxt;
+      const int in = (c + 1) * NT + t;
+      nxt = in < mk ? ids[in] : -1;
       lds_barrier();
       // fold the previous chunk's per-wave counts into the per-expert base, then rank this one
 #pragma unroll
@@ -775,7 +780,7 @@ __global__ __launch_bounds__(NT) void lru_k(
           L.ecnt[x] += add;
         }
       }
-      e = i < mk ? ids[i] : -1;
+      e = i < mk ? cur : -1;
       v = e >= 0 && e < E;
       lds_barrier();
       const uint64_t m = match_any(e, v, kbits);
@@ -882,7 +887,7 @@ __global__ __launch_bounds__(NT) void split_fresh_k(const int* __restrict__ eids
 // the others (start left at L) write nothing.
 constexpr int PT = 1024;            // threads and tokens of one placement workgroup
 constexpr int PWV = PT / WAVE;
-constexpr int PLACE_MIN = 2048;     // the fused launch defers placement above this many tokens
+constexpr int PLACE_MIN = 1536;     // the fused launch defers placement above this many tokens
 constexpr int PLOADS = 8;           // id loads in flight per thread while counting (unaligned)
 constexpr int PB = 4;               // expert-id blocks per thread in flight
 

@@ -263,7 +263,8 @@ def test_fused_geometries(mine, rows):
 
 PLACE_CASES = [
     # (tag, mk, bs, L override, NB override, invalid-id fraction)
-    ("just-past-threshold", 2049, 16, None, None, 0.0),
+    ("just-past-threshold", 1537, 16, None, None, 0.0),
+    ("past-threshold-2049", 2049, 16, None, None, 0.0),
     ("ragged-with-invalid-ids", 9001, 16, None, None, 0.05),
     # fewer expert-id blocks than L needs (the library bounds the writes; the reference
     # writes past them): the single-workgroup placement
@@ -277,7 +278,7 @@ PLACE_CASES = [
 
 @pytest.mark.parametrize("case", PLACE_CASES, ids=[c[0] for c in PLACE_CASES])
 def test_fused_parallel_placement(mine, case):
-    """Above 2048 tokens the align's tokens are ranked by many workgroups; the outputs and the
+    """Above 1536 tokens the align's tokens are ranked by many workgroups; the outputs and the
     state stay bit-exact against the oracle: ids outside [0, E) skipped, a runtime block size,
     and a short expert-id array (NB * bs < L), which keeps the single-workgroup placement."""
     tag, mk, bs, L, NB, bad = case
