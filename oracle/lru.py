@@ -16,7 +16,12 @@ Parity pins (tests/test_oracle_lru.py):
     19 cases of tests/lru/test_victim_equiv.py:137-159;
   * against brute force (every permutation / every subset) on tiny E and S;
   * against the invariants of tests/lru/test_lru.py:138-145 and test_slots_prod.py:183-197;
-  * against the committed golden fixtures (tests/golden/).
+  * against the committed golden fixtures (tests/golden/);
+  * warm_start(): hand-worked states for a 5-slot profile (stamps, slots, table, step, cap,
+    read-through threshold), the first evictions after it taking the profile's coldest slots,
+    and the edges (no profile, S = 1, experts missing from the profile, S = 257);
+  * align_sizes(): against the worst num_post_pad over every routing of tiny E / mk / bs
+    (brute force): L holds it and exceeds it by (mk - E) mod bs at most.
 Align order: stable (ascending token index inside a bucket) at every mk. That equals the
 reference's deterministic path (mk <= 256, r4d_lru.hip:542-562) and is one member of the
 per-bucket multiset class its atomic-cursor path (mk > 256) produces.

@@ -181,6 +181,136 @@ def test_brute_force_victims_tiny():
         assert s.miss[:got, 1].tolist() == want, trial
 
 
+# ---- warm start (_build_lru, r4d_mxfp4_moe.py.lru.diff:502-541): hand-worked answers -------
+# E = 8, hot set {6, 1, 4, 3, 7}; the layer's profile ranks experts 4, 7, 1, 6, 3, 0, 2, 5
+# (0 = most often routed). Slots take the hot ids in ascending order: [1, 3, 4, 6, 7]. The
+# hottest (4, slot 2) gets stamp S = 5, then 7 (slot 4) 4, 1 (slot 0) 3, 6 (slot 3) 2 and the
+# coldest, 3 (slot 1), 1. Every value below was worked out by hand from that rule.
+WS_HOT = [6, 1, 4, 3, 7]
+WS_RANK = {e: i for i, e in enumerate([4, 7, 1, 6, 3, 0, 2, 5])}
+
+
+def test_known_answer_warm_start_profile():
+    s = lru.warm_start(8, 5, WS_HOT, WS_RANK)
+    assert s.slot_expert.tolist() == [1, 3, 4, 6, 7]
+    assert s.slot_stamp.tolist() == [3, 1, 5, 2, 4]
+    assert s.table.tolist() == [-1, 0, -1, 1, 2, -1, 3, 4]
+    assert s.map_cold.tolist() == [0, -1, 2, -1, -1, 5, -1, -1]
+    assert s.step.tolist() == [5]
+    assert s.max_distinct == 2                  # max(1, int(5 * 0.5))
+    assert s.max_inserts == 5 and s.miss.shape == (5, 2)   # cap = min(64, S)
+    assert (s.miss == -1).all() and s.n_miss.tolist() == [0]
+    assert not lru.check_invariants(s)
+
+
+def test_known_answer_warm_start_evicts_coldest_first():
+    """The first misses after a warm start take the profile's coldest slots, in rank order:
+    a stamp rule turned upside down would evict the hottest expert (4) first."""
+    s = lru.warm_start(8, 5, WS_HOT, WS_RANK)
+    s.max_distinct = 8
+    assert lru.manage(s, np.array([0, 4])) == 1     # 4 hits (slot 2), 0 misses
+    assert s.miss[0].tolist() == [0, 1]              # into slot 1: expert 3, stamp 1
+    assert s.slot_expert.tolist() == [1, 0, 4, 6, 7]
+    assert s.slot_stamp.tolist() == [3, 6, 6, 2, 4]
+    assert lru.manage(s, np.array([2, 5])) == 2      # next oldest: slot 3 (2), slot 0 (3)
+    assert s.miss[:2].tolist() == [[2, 3], [5, 0]]
+    c = lru.warm_start(8, 5, WS_HOT, WS_RANK)
+    c.max_distinct = 8
+    clru.manage(c, np.array([0, 4]))
+    clru.manage(c, np.array([2, 5]))
+    same_state(s, c)
+
+
+def test_known_answer_warm_start_edges():
+    # no profile: zero stamps, so ties go by slot (lowest id first); S = 1 reads through above 1
+    s = lru.warm_start(8, 3, [5, 2, 7], None)
+    assert s.slot_expert.tolist() == [2, 5, 7] and s.slot_stamp.tolist() == [0, 0, 0]
+    assert s.max_distinct == 1 and s.step.tolist() == [3]
+    one = lru.warm_start(4, 1, [3], {3: 0})
+    assert one.slot_stamp.tolist() == [1] and one.max_distinct == 1 and one.max_inserts == 1
+    # experts missing from the profile rank after every ranked one (rank = len(rank)), so
+    # they get the lowest stamps; among themselves, slot order
+    part = lru.warm_start(8, 4, [0, 2, 5, 6], {6: 0, 2: 1})
+    assert part.slot_stamp.tolist() == [2, 3, 1, 4]
+    # the production geometry: S = 257 -> max_distinct 128, cap 64, stamps a permutation of
+    # 1..257 with the hottest at S
+    rank = {e: i for i, e in enumerate(np.random.default_rng(7).permutation(512).tolist())}
+    hot = sorted(rank, key=rank.get)[:257]
+    big = lru.warm_start(512, 257, hot, rank)
+    assert big.max_distinct == 128 and big.max_inserts == 64
+    assert sorted(big.slot_stamp.tolist()) == list(range(1, 258))
+    hottest = min(hot, key=rank.get)
+    assert big.slot_stamp[big.table[hottest]] == 257
+    assert list(big.slot_expert) == sorted(hot)
+
+
+def test_product_warm_start_known_answer():
+    """LruCache.build (the product's _build_lru) on the CPU gives the hand-worked state."""
+    c = load_pkg().LruCache.build(8, WS_HOT, WS_RANK, "cpu")
+    assert c.slot_expert.tolist() == [1, 3, 4, 6, 7]
+    assert c.slot_stamp.tolist() == [3, 1, 5, 2, 4]
+    assert c.table.tolist() == [-1, 0, -1, 1, 2, -1, 3, 4]
+    assert c.map_cold.tolist() == [0, -1, 2, -1, -1, 5, -1, -1]
+    assert c.step.tolist() == [5] and c.max_distinct == 2 and c.max_inserts == 5
+    assert tuple(c.miss.shape) == (5, 2)
+
+
+def test_planted_warm_start_mistakes_are_caught():
+    """Reversed stamps, unsorted slots and a wrong step each fail the hand-worked answers."""
+    good = lru.warm_start(8, 5, WS_HOT, WS_RANK)
+    rev = good.copy()
+    rev.slot_stamp[:] = 6 - good.slot_stamp              # hottest -> 1, coldest -> S
+    assert rev.slot_stamp.tolist() != [3, 1, 5, 2, 4]
+    rev.max_distinct = 8
+    lru.manage(rev, np.array([0, 4]))
+    assert rev.miss[0].tolist() == [0, 4]                # evicts expert 7 (2nd hottest), not 3
+    unsorted = lru.make_state(8, 5, WS_HOT, good.slot_stamp, step=5)
+    assert unsorted.slot_expert.tolist() != [1, 3, 4, 6, 7]
+
+
+# ---- align sizes (r4d_mxfp4_moe.py.lru.diff:290-296): the worst case, by brute force -------
+def _worst_npad(mk: int, E: int, bs: int) -> int:
+    """Largest num_post_pad any routing of mk ids (each in [-1, E)) can produce, over every
+    multiset of ids."""
+    best = 0
+    for ids in itertools.combinations_with_replacement(range(-1, E), mk):
+        cnt = np.bincount(np.array([i for i in ids if i >= 0], np.int64), minlength=E)
+        best = max(best, int(((cnt + bs - 1) // bs * bs).sum()))
+    return best
+
+
+@pytest.mark.parametrize("E", [1, 2, 3, 5])
+@pytest.mark.parametrize("bs", [1, 2, 4, 16])
+def test_align_sizes_brute_force(E, bs):
+    """L must hold the worst routing's padded run (else the kernel would write past it), and
+    be tight: it exceeds that worst case by (mk - E) mod bs < bs when mk >= E, by nothing
+    when mk < E. NB = ceil(L / bs) blocks."""
+    for mk in range(1, 8):
+        L, NB = lru.align_sizes(mk, E, bs)
+        worst = _worst_npad(mk, E, bs)
+        assert worst <= L, (mk, E, bs)
+        assert L - worst == ((mk - E) % bs if mk >= E else 0), (mk, E, bs, L, worst)
+        assert (NB - 1) * bs < L <= NB * bs
+        # the worst routing through the oracle's align fills exactly `worst` entries
+        if mk < E:
+            ids = np.arange(mk)
+        else:
+            extra = (mk - E) // bs * bs
+            ids = np.concatenate([np.arange(E), np.zeros(extra, np.int64),
+                                  np.full(mk - E - extra, -1)])
+        out = lru.align(ids, E, E, np.arange(E, dtype=np.int32), bs, L, NB)
+        assert int(out[2][0]) == worst and int(out[5][0]) == 0
+
+
+def test_align_sizes_known_answers():
+    # C1 / C2: 5 tokens x top-10 over 512 experts; C3: 20 tokens; a 4096-token prefill chunk
+    assert lru.align_sizes(50, 512, 16) == (800, 50)
+    assert lru.align_sizes(200, 512, 16) == (3200, 200)
+    assert lru.align_sizes(40960, 512, 16) == (40960 + 512 * 15, (40960 + 512 * 15) // 16)
+    assert lru.align_sizes(512, 512, 16) == (512 + 512 * 15, 512)
+    assert lru.align_sizes(7, 3, 4) == (16, 4)
+
+
 # ---- planted mistakes must be caught ------------------------------------------------------
 def _planted(kind):
     """A copy of the numpy manager with one plausible mistake."""
