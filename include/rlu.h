@@ -20,7 +20,10 @@ extern "C" {
 
 /* ---- device LRU expert cache -------------------------------------------------------------
  * Replaces kernels/lru/r4d_lru.hip:579-589 (r4d_lru_manage), :596-610 (r4d_lru_fused) and
- * :612-629 (r4d_lru_gather) with identical signatures, argument meaning and return codes.
+ * :612-629 (r4d_lru_gather) with identical signatures and argument meaning. The return codes
+ * are the reference's with one narrower limit: r4d_lru_manage also returns -1 for E > 1024
+ * (the reference's manager took any E; its fused kernel, like both here, stops at 1024, and the
+ * 512-expert model is far inside it). A negative mk means no tokens, as in the reference.
  * Bound from Python as in patches/.../fused_moe/experts/r4d_mxfp4_moe.py.lru.diff:184-200:
  *   manage: [void*] + [int]*5 + [void*]*9
  *   fused:  [void*] + [int]*5 + [void*]*8 + [int]*3 + [void*]*7
@@ -30,10 +33,10 @@ extern "C" {
  * map_cold[E] int32 expert->expert when not resident else -1, slot_expert[S] int32,
  * slot_stamp[S] int64, routed[E] uint8 (scratch, left holding this step's routed flags),
  * step[1] int64, miss[cap][2] int32 (expert, slot), n_miss[1] int32.
- * Limits: 1 <= E <= 1024, 1 <= S <= 1024, 0 <= max_inserts <= 1024, mk >= 0.
- * Returns -1 outside them. fused additionally needs bs, L, NB > 0; L and NB must be the sizes
- * moe_align_block_size allocates (L = mk < E ? min(mk*bs, mk+E*(bs-1)) : mk+E*(bs-1),
- * NB = ceil(L/bs)); writes past L / NB are dropped rather than performed.
+ * Limits: 1 <= E <= 1024, 1 <= S <= 1024, 0 <= max_inserts <= 1024 (and mk >= 0 for fused).
+ * Returns -1 outside them; manage treats mk < 0 as mk = 0. fused additionally needs bs, L,
+ * NB > 0; L and NB must be the sizes moe_align_block_size allocates
+ * (L = mk < E ? min(mk*bs, mk+E*(bs-1)) : mk+E*(bs-1), NB = ceil(L/bs)); writes past L / NB are dropped rather than performed.
  * Align output order is stable (ascending token index inside each bucket) at every mk.
  * gather: every size must be > 0 and a multiple of 16, chunks and lanes > 0; grid is
  * (chunks, lanes); sources may be pinned host memory (device pointer from
@@ -186,6 +189,18 @@ int rlu_moe_gemm_fp8blk_tiled(const void* qx, const float* xs, const void* wq, c
  * -2 K % 128, N % 32 or K > 4096. */
 int rlu_gemm_w4_m16(const void* x, int M, int K, const void* wq, const unsigned* sz, void* y,
                     int N, int wv, hipStream_t stream);
+
+/* Replaces quantize_w4 + pack_w4a16 (kernels/draft_w4_lmhead.py:154-198,228-259), with this
+ * build's own quantizer, in the format rlu_gemm_w4_m16 reads: w [N, K] (row stride ld elements,
+ * 16-byte aligned rows; dtype 0 bf16, 1 f32, 2 f16) -> wq [n_pad/16][K/128][64][16] codes and
+ * sz [n_pad/16][K/128][16] words; rows N..n_pad-1 are packed as zeros. Per (row, 128-column
+ * group): 10 clip fractions f of the range (s = bf16(f (hi - lo) / 15)) x the centred integer
+ * zero and its two neighbours, codes clamp(rint(w / s) + z, 0, 15), least squared error (summed
+ * in a fixed order) wins; a constant group stores s = bf16(|v|). Deterministic: the same bytes on
+ * every run. Returns -1 bad sizes or null pointers, -2 K % 128 or n_pad % 16, -3 bad dtype,
+ * -4 misaligned w / ld / wq / sz. */
+int rlu_pack_w4(const void* w, int dtype, long long ld, int N, int K, int n_pad, void* wq,
+                unsigned* sz, hipStream_t stream);
 
 /* Replaces the capture fn of tools/routecap/routecap.py:83-100 (five torch ops per layer
  * there, one launch here; safe to record into a HIP graph). Copies one MoE layer's n routed

@@ -199,8 +199,12 @@ def block_quant_weight(w: np.ndarray, blk: int = 128) -> tuple[np.ndarray, np.nd
 
 
 def dequant_weight(wq: np.ndarray, ws: np.ndarray, blk: int = 128) -> np.ndarray:
+    """e4m3 [N, K] x its [N/blk, K/blk] block scales -> float32 (one product per weight)."""
     v = e4m3_to_f32(wq)
-    return v * np.repeat(np.repeat(ws, blk, 0), blk, 1)
+    N, K = v.shape
+    b = v.reshape(N // blk, blk, K // blk, blk)
+    b *= np.asarray(ws, np.float32)[:, None, :, None]
+    return v
 
 
 def dequant_act(q: np.ndarray, scale: np.ndarray) -> np.ndarray:

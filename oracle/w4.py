@@ -1,17 +1,30 @@
 """W4 (int4 group-128, asymmetric) quantizer, layout and GEMV reference (test infrastructure).
 
+This build's W4 format stores w ~ scale * (q - zero) per (row, 128-column group) with a bf16
+scale and an integer zero, where the reference stored an f16 scale (kernels/draft_w4_lmhead.py:
+31-50, quantize_w4 :154-198). The quantizer is this build's own: the reference's codes are not
+reachable with a bf16 scale, and its module imports vLLM (absent), so the reference's exact
+codes stay parity unpinned; the format and the kernel are pinned against this restatement.
+
 Functions and what pins them (tests/test_oracle_w4.py):
-  quantize_w4()  kernels/draft_w4_lmhead.py:154-198 restated in numpy float32, with the scale
-                 rounded to bf16 (this build's format) where the reference rounds to f16: per
-                 (row, group) and clip fraction c of the reference grid (:151), scale =
-                 bf16((hi_c - lo_c) / 15), a constant nonzero group gets bf16(|lo| / 7) and zero
-                 8, zero = round(-lo_c / scale) clamped to +-1024, q = clamp(round(w / scale +
-                 zero), 0, 15), the least squared error wins. Pinned by closed forms: every
-                 code is the nearest grid point of its (scale, zero) unless clamped; the chosen
-                 clip has the least error of the grid (brute force in float64); plain min/max
-                 on Gaussian weights lands at the textbook ~0.104 sigma RMS error the reference
-                 quotes (:143-150). The reference's exact codes (f16 scale) are parity unpinned:
-                 its module imports vLLM, which is absent.
+  quantize_w4()  per (row, group) with range width = hi - lo and centre mid = (lo + hi) / 2:
+                 for each fraction f of FRACTIONS (1.0 down to 0.55), scale s = bf16(f * width
+                 / 15), centred zero z0 = rint(7.5 - mid / s), and each zero z of z0, z0 - 1,
+                 z0 + 1 (clamped to +-1024): codes q = clamp(rint(w / s) + z, 0, 15), error =
+                 sum of ((q - z) s - w)^2 summed in ERR_ORDER; the first candidate with the
+                 least error wins. A constant group (width 0) stores s = bf16(|v|), z = 1 for a
+                 negative v and 0 otherwise (an all-zero group: s = 0, z = 0, codes 0). Every
+                 operation is one float32 rounding, as the packing kernel computes it.
+                 Pinned by closed forms (each code is the nearest grid point of its (s, z) unless
+                 clamped; each constant group decodes to bf16(v)), by brute force (the chosen
+                 candidate has the least float64 error of all 30, up to float32 rounding), and
+                 by the error level on Gaussian weights: plain min/max at the textbook ~0.104
+                 sigma RMS of a 16-level grid over the ~5.4 sigma range of 128 samples, the
+                 search below it.
+  ERR_ORDER      lane l = 16 c + r of the tile's wave holds row r's 32 values k = 32 i + 8 c + j
+                 (i, j ascending, the order they sit in its packed dwords); each lane sums its 32
+                 squared errors in that order, then the four lanes of a row combine as
+                 (p_0 + p_1) + (p_2 + p_3) -- every lane of the row gets the same float.
   pack_codes() / unpack_codes() / pack_sz()  this build's layout: [N/16][K/128][64 lanes][16 B],
                  lane 16 c + r = row r, dword i = 32-deep step i, k = 128 g + 32 i + 8 c + j,
                  nibble t of the low half = j 2t, nibble t of the high half = j 2t + 1; sz =
@@ -24,40 +37,77 @@ import numpy as np
 
 from . import fp8
 
-CLIP_GRID = (1.0, 0.95, 0.9, 0.85, 0.8, 0.75, 0.7, 0.65, 0.6)
 GROUP = 128
+# clip fractions of the group's range, by their float32 bits (1.0, 0.95, ..., 0.55)
+FRACTION_BITS = (0x3F800000, 0x3F733333, 0x3F666666, 0x3F59999A, 0x3F4CCCCD,
+                 0x3F400000, 0x3F333333, 0x3F266666, 0x3F19999A, 0x3F0CCCCD)
+FRACTIONS = tuple(np.uint32(b).view(np.float32) for b in FRACTION_BITS)
+ZERO_SHIFTS = (0, -1, 1)
+ZMAX = 1024
 
 
-def quantize_w4(w: np.ndarray, group: int = GROUP, clip_grid=None):
+def _lanes(w: np.ndarray, group: int) -> np.ndarray:
+    """[N, K] -> [N, G, 4 (c), 32 (i, j)]: the values each lane of a tile's wave holds."""
+    n, k = w.shape
+    return w.reshape(n, k // group, 4, 4, 8).transpose(0, 1, 3, 2, 4).reshape(n, k // group, 4, 32)
+
+
+def _unlanes(t: np.ndarray) -> np.ndarray:
+    n, g = t.shape[:2]
+    return t.reshape(n, g, 4, 4, 8).transpose(0, 1, 3, 2, 4).reshape(n, g * 128)
+
+
+def lane_error(d2: np.ndarray) -> np.ndarray:
+    """Sum [.., 4, 32] float32 squared errors in ERR_ORDER -> [..] float32."""
+    p = d2[..., 0].copy()
+    for m in range(1, 32):
+        p = p + d2[..., m]
+    return (p[..., 0] + p[..., 1]) + (p[..., 2] + p[..., 3])
+
+
+def quantize_w4(w: np.ndarray, group: int = GROUP, fractions=None, shifts=None):
     """[N, K] -> (q uint8 [N, K], scale float32 (bf16 values) [N, G], zero int16 [N, G])."""
+    assert group == GROUP
     w = np.asarray(w, np.float32)
     n, k = w.shape
-    wf = w.reshape(n, k // group, group)
-    lo, hi = wf.min(-1), wf.max(-1)
-    f = np.float32
-    mid, half = (hi + lo) / f(2), (hi - lo) / f(2)
+    t = _lanes(w, group)
+    lo = w.reshape(n, k // group, group).min(-1)
+    hi = w.reshape(n, k // group, group).max(-1)
+    width = hi - lo
+    mid = (lo + hi) / np.float32(2)
     best_err = np.full(lo.shape, np.inf, np.float32)
-    best_scale = np.zeros(lo.shape, np.float32)
-    best_zero = np.zeros(lo.shape, np.float32)
-    for c in (clip_grid if clip_grid is not None else CLIP_GRID):
-        c = f(c)
-        lo_c, hi_c = mid - c * half, mid + c * half
-        scale = fp8.bf16_round(np.maximum((hi_c - lo_c) / f(15.0), f(0.0)))
-        flat = (scale == 0) & (lo != 0)
-        scale = np.where(flat, fp8.bf16_round(np.abs(lo) / f(7.0)), scale).astype(np.float32)
-        with np.errstate(divide="ignore"):
-            inv = np.where(scale > 0, f(1.0) / np.maximum(scale, f(1e-30)), f(0.0)).astype(np.float32)
-        zero = np.clip(np.where(flat, f(8.0), np.round(-lo_c * inv)), -1024, 1024).astype(np.float32)
-        q = np.clip(np.round(wf * inv[..., None] + zero[..., None]), 0, 15).astype(np.float32)
-        err = np.square((q - zero[..., None]) * scale[..., None] - wf).sum(-1, dtype=np.float32)
-        take = err < best_err
-        best_err = np.where(take, err, best_err)
-        best_scale = np.where(take, scale, best_scale)
-        best_zero = np.where(take, zero, best_zero)
-    with np.errstate(divide="ignore"):
-        inv = np.where(best_scale > 0, f(1.0) / np.maximum(best_scale, f(1e-30)), f(0.0)).astype(np.float32)
-    q = np.clip(np.round(wf * inv[..., None] + best_zero[..., None]), 0, 15)
-    return q.astype(np.uint8).reshape(n, k), best_scale, best_zero.astype(np.int16)
+    best_s = np.zeros(lo.shape, np.float32)
+    best_z = np.zeros(lo.shape, np.float32)
+    best_q = np.zeros(t.shape, np.float32)
+    for f in (FRACTIONS if fractions is None else fractions):
+        s = fp8.bf16_round((np.float32(f) * width) / np.float32(15))
+        ok = (s > 0) & (width > 0)
+        ss = np.where(ok, s, np.float32(1))
+        u = np.rint(t / ss[..., None, None])
+        z0 = np.clip(np.rint(np.float32(7.5) - mid / ss), -ZMAX, ZMAX)
+        for dz in (ZERO_SHIFTS if shifts is None else shifts):
+            z = np.clip(z0 + np.float32(dz), -ZMAX, ZMAX)
+            q = np.clip(u + z[..., None, None], 0, 15)
+            d = (q - z[..., None, None]) * ss[..., None, None] - t
+            err = np.where(ok, lane_error(d * d), np.float32(np.inf))
+            take = err < best_err
+            best_err = np.where(take, err, best_err)
+            best_s = np.where(take, s, best_s)
+            best_z = np.where(take, z, best_z)
+            best_q = np.where(take[..., None, None], q, best_q)
+    # constant groups
+    const = width == 0
+    sc = fp8.bf16_round(np.abs(lo))
+    zc = np.where(lo < 0, np.float32(1), np.float32(0))
+    scs = np.where(sc > 0, sc, np.float32(1))
+    qc = np.where((sc > 0)[..., None, None],
+                  np.clip(np.rint(t / scs[..., None, None]) + zc[..., None, None], 0, 15),
+                  np.float32(0))
+    best_s = np.where(const, sc, best_s)
+    best_z = np.where(const, np.where(sc > 0, zc, np.float32(0)), best_z)
+    best_q = np.where(const[..., None, None], qc, best_q)
+    return (_unlanes(best_q).astype(np.uint8), best_s.astype(np.float32),
+            best_z.astype(np.int16))
 
 
 def dequant(q: np.ndarray, scale: np.ndarray, zero: np.ndarray, group: int = GROUP) -> np.ndarray:

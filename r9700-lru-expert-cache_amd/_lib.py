@@ -34,6 +34,7 @@ SIGNATURES: dict[str, tuple] = {
     "rlu_moe_gemm_split": (_I, [_P] * 14 + [_I] * 8 + [_P]),
     "rlu_shuffle_fp8_weight": (_I, [_P, _P, _LL, _I, _P]),
     "rlu_gemm_w4_m16": (_I, [_P, _I, _I, _P, _P, _P, _I, _I, _P]),
+    "rlu_pack_w4": (_I, [_P, _I, _LL, _I, _I, _I, _P, _P, _P]),
     "rlu_moe_gemm_tiles": (_I, [_P, _P, _I, _P, _P, _P]),
     "rlu_moe_gemm_fp8blk_tiled": (_I, [_P] * 8 + [_I, _P, _P] + [_I] * 5 + [_P]),
     "rlu_route_capture": (_I, [_P] + [_I] * 5 + [_P] * 4),
@@ -70,3 +71,33 @@ def stream_ptr(stream=None) -> int:
 def check(rc: int, what: str) -> None:
     if rc != 0:
         raise RuntimeError(f"{what} failed rc={rc}")
+
+
+@functools.lru_cache(maxsize=1)
+def _hip():
+    return ctypes.CDLL("libamdhip64.so")
+
+
+@functools.lru_cache(maxsize=4096)
+def _pinned_device_ptr(host_ptr: int) -> int:
+    dp = ctypes.c_void_p()
+    rc = _hip().hipHostGetDevicePointer(ctypes.byref(dp), ctypes.c_void_p(host_ptr),
+                                        ctypes.c_uint(0))
+    if rc != 0:
+        raise RuntimeError(f"hipHostGetDevicePointer rc={rc}")
+    return dp.value
+
+
+def device_ptr_of_pinned(t) -> int:
+    """Device-visible address of a pinned host tensor (UVA); looked up once per address."""
+    return _pinned_device_ptr(t.data_ptr())
+
+
+def device_ptr(t) -> int:
+    """The address a kernel uses for `t`: its own for device memory, the device-visible one
+    for pinned host memory. Anything else (pageable host memory) is refused."""
+    if t.is_cuda:
+        return t.data_ptr()
+    if t.is_pinned():
+        return device_ptr_of_pinned(t)
+    raise ValueError("operand must be device memory or pinned host memory")

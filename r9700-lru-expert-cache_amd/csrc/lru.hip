@@ -1050,7 +1050,8 @@ int r4d_lru_manage(const int* topk_ids, int mk, int E, int S, int max_distinct,
                    long long* slot_stamp, unsigned char* routed, long long* step, int* miss,
                    int* n_miss, hipStream_t stream) {
   if (E <= 0 || E > rlu::MAXE || S <= 0 || S > rlu::MAXS) return -1;
-  if (max_inserts < 0 || max_inserts > rlu::MAXINS || mk < 0) return -1;
+  if (max_inserts < 0 || max_inserts > rlu::MAXINS) return -1;
+  if (mk < 0) mk = 0;     // the reference's loops over mk ids run zero times
   hipLaunchKernelGGL(rlu::lru_k<false>, dim3(1), dim3(rlu::NT), 0, stream, topk_ids, mk, E, S,
                      max_distinct, max_inserts, table, map_cold, slot_expert, slot_stamp,
                      routed, step, miss, n_miss, 1, 0, 0, nullptr, nullptr, nullptr, nullptr,

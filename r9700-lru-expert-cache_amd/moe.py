@@ -20,22 +20,11 @@ from dataclasses import dataclass
 import torch
 
 from . import ops
-from ._lib import check, lib, stream_ptr
+from ._lib import check, device_ptr_of_pinned, lib, stream_ptr  # noqa: F401
 from .lru import LRU_CHUNKS, LRU_LANES, LruCache, _r4d_lru_gather, split_fresh
 
 _P = ctypes.c_void_p
 BLOCK = 16
-
-
-def device_ptr_of_pinned(t: torch.Tensor) -> int:
-    """Device-visible address of a pinned host tensor (UVA)."""
-    hip = ctypes.CDLL("libamdhip64.so")
-    dp = ctypes.c_void_p()
-    rc = hip.hipHostGetDevicePointer(ctypes.byref(dp), ctypes.c_void_p(t.data_ptr()),
-                                     ctypes.c_uint(0))
-    if rc != 0:
-        raise RuntimeError(f"hipHostGetDevicePointer rc={rc}")
-    return dp.value
 
 
 @dataclass

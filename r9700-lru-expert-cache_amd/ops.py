@@ -26,7 +26,7 @@ import os
 
 import torch
 
-from ._lib import check, lib, stream_ptr
+from ._lib import check, device_ptr, lib, stream_ptr
 
 _P = ctypes.c_void_p
 FP8 = torch.float8_e4m3fn
@@ -95,7 +95,8 @@ def _r4d_fp8_moe_gemm_into(y: torch.Tensor, qx: torch.Tensor, x_scale: torch.Ten
                            num_post_pad: torch.Tensor, topk_weights: torch.Tensor | None,
                            mtk: int, top_k: int, wv: int, sk: int, npw: int) -> None:
     """The grouped GEMM writing into caller-owned y: only rows named in sorted_ids are
-    touched, so hot and cold subsets fill one buffer."""
+    touched, so hot and cold subsets fill one buffer. wq / ws_t may be device memory (the
+    slots) or pinned host memory (the full expert tensor, read over the host link)."""
     K = qx.shape[1]
     N = wq.shape[1]
     assert y.shape == (mtk, N) and y.dtype == torch.bfloat16 and y.is_contiguous()
@@ -104,10 +105,24 @@ def _r4d_fp8_moe_gemm_into(y: torch.Tensor, qx: torch.Tensor, x_scale: torch.Ten
     assert sorted_ids.dtype == torch.int32 and expert_ids.dtype == torch.int32
     em = sorted_ids.numel()
     rc = lib().r4d_gemm_moe_fp8blk_nt_b16(
-        _p(qx), _p(x_scale), _p(wq), _p(ws_t), _p(wref), _p(y), _p(sorted_ids),
-        _p(expert_ids), _p(num_post_pad), _p(topk_weights), em, mtk, top_k, K, N, wv, sk, npw,
-        _P(stream_ptr()))
+        _p(qx), _p(x_scale), _P(device_ptr(wq)), _P(device_ptr(ws_t)), _p(wref), _p(y),
+        _p(sorted_ids), _p(expert_ids), _p(num_post_pad), _p(topk_weights), em, mtk, top_k, K,
+        N, wv, sk, npw, _P(stream_ptr()))
     check(rc, "r4d_gemm_moe_fp8blk_nt_b16")
+
+
+def _r4d_fp8_moe_gemm(qx: torch.Tensor, x_scale: torch.Tensor, wq: torch.Tensor,
+                      ws_t: torch.Tensor, wref: torch.Tensor | None, sorted_ids: torch.Tensor,
+                      expert_ids: torch.Tensor, num_post_pad: torch.Tensor,
+                      topk_weights: torch.Tensor | None, mtk: int, top_k: int, wv: int,
+                      sk: int, npw: int) -> torch.Tensor:
+    """The allocating form the reference's single-call path uses (r4d_mxfp4_moe.py.lru.diff:
+    625,635): a new y [mtk, N] bf16. Rows no block of sorted_ids names are left as allocated
+    (torch.empty); with one align over every expert, every valid (token, k) row is named."""
+    y = torch.empty((mtk, wq.shape[1]), dtype=torch.bfloat16, device=qx.device)
+    _r4d_fp8_moe_gemm_into(y, qx, x_scale, wq, ws_t, wref, sorted_ids, expert_ids,
+                           num_post_pad, topk_weights, mtk, top_k, wv, sk, npw)
+    return y
 
 
 def gemm_fp8_block_q(qx: torch.Tensor, xs: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor,
@@ -231,3 +246,27 @@ def moe_gemm_tiled(y: torch.Tensor, qx: torch.Tensor, x_scale: torch.Tensor, wq:
         _P(tiles.data_ptr() + 8 * nb), nb, _p(topk_weights), _p(y), mtk, top_k, K, N, wv,
         _P(stream_ptr()))
     check(rc, "rlu_moe_gemm_fp8blk_tiled")
+
+
+# ---- torch custom ops at the reference's names and schemas ----------------------------------
+# r4d_mxfp4_moe_gemm_into / r4d_mxfp4_moe_gemm: patches/.../r4d_mxfp4_moe.py.lru.diff:363-423
+# (mutates_args=["y"], a fake impl) and the allocating call sites :625,635. Registered in the
+# namespace the LRU ops use ("vllm" when vLLM is importable, else "rlu").
+def _register():
+    from .lru import OPS_NAMESPACE
+    lib_ = torch.library.Library(OPS_NAMESPACE, "FRAGMENT")
+    args = ("Tensor qx, Tensor x_scale, Tensor wq, Tensor ws_t, Tensor? wref, "
+            "Tensor sorted_ids, Tensor expert_ids, Tensor num_post_pad, "
+            "Tensor? topk_weights, int mtk, int top_k, int wv, int sk, int npw")
+    lib_.define(f"r4d_mxfp4_moe_gemm_into(Tensor(a!) y, {args}) -> ()")
+    lib_.define(f"r4d_mxfp4_moe_gemm({args}) -> Tensor")
+    lib_.impl("r4d_mxfp4_moe_gemm_into", _r4d_fp8_moe_gemm_into, "CUDA")
+    lib_.impl("r4d_mxfp4_moe_gemm", _r4d_fp8_moe_gemm, "CUDA")
+    lib_.impl("r4d_mxfp4_moe_gemm_into", lambda *a, **k: None, "Meta")
+    lib_.impl("r4d_mxfp4_moe_gemm",
+              lambda qx, xs, wq, *a: torch.empty((a[6], wq.shape[1]), dtype=torch.bfloat16,
+                                                  device=qx.device), "Meta")
+    return lib_
+
+
+_OPS_LIB = _register()

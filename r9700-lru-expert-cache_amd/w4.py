@@ -1,23 +1,25 @@
 """W4 draft lm_head: int4 group-128 weights, bf16 activations, bf16 logits, on librlu.so.
 
 Mirrors kernels/draft_w4_lmhead.py: PackedW4 (:63-76), quantize_w4 (:154-198), pack_w4a16
-(:228-259), unpack_w4 (:262-285), gemm_w4a16 (:393-403), in this build's gfx950 format:
+(:228-259), unpack_w4 (:262-285), the op draft_w4_lmhead_gemm (:351-390) and gemm_w4a16
+(:393-403), in this build's gfx950 format:
 
   codes  q in 0..15 per weight, w ~ scale * (q - zero) per (row, 128-column group), asymmetric,
-         the integer zero in [-1024, 1024] (a constant or all-positive group needs one outside
-         0..15), the scale rounded to bf16 BEFORE the codes are chosen so the packed weight is
-         exactly what the kernel reads, the clip fraction chosen per (row, group) by squared
-         error over the reference's grid (:151).
+         a bf16 scale and an integer zero in [-1024, 1024] (a constant or all-positive group
+         needs one outside 0..15).
   wq     uint8 [N_pad/16, K/128, 64, 16]: the 1 KB of a 16-row x 128-deep tile in
          v_mfma_f32_16x16x32_bf16 B-operand order (lane 16 c + r holds row r, four dwords, one
          per 32-deep step i, k = 128 g + 32 i + 8 c + j; nibble t of the low half is j = 2t,
          nibble t of the high half is j = 2t + 1).
   sz     int32 [N_pad/16, K/128, 16]: bf16 scale bits | int16 zero << 16.
 
-The reference stores an f16 scale and widens bf16 activations to f16 for its gfx1201 WMMA;
-here the activations stay bf16 and the scale is bf16. N is padded to a multiple of 32 (the
-kernel's item is two 16-row strips) with zero rows (scale 0), sliced off again by gemm_w4a16.
-M > 16 runs the kernel on 16-row slices.
+Quantizing and packing is one kernel (rlu_pack_w4): a wave per 16-row x 128-column tile, each
+lane choosing the codes of the nibbles it stores. Per (row, group) it tries 10 clip fractions of
+the group's range (bf16 scale) and, for each, the centred integer zero and its two neighbours,
+and keeps the least squared error; a constant group is stored exactly up to the bf16 scale.
+The reference stores an f16 scale and widens bf16 activations to f16 for its gfx1201 WMMA; here
+the activations stay bf16. N is padded to a multiple of 32 (the GEMV's item is two 16-row
+strips) with zero rows, sliced off again by the op. M > 16 runs the kernel on 16-row slices.
 """
 from __future__ import annotations
 
@@ -27,12 +29,13 @@ from dataclasses import dataclass
 import torch
 
 from ._lib import check, lib, stream_ptr
+from .lru import OPS_NAMESPACE as OPS_NS
 
 GROUP = 128
 MAX_M = 16
 N_ALIGN = 32         # the kernel's item is two 16-row strips
-CLIP_GRID = (1.0, 0.95, 0.9, 0.85, 0.8, 0.75, 0.7, 0.65, 0.6)
 _P = ctypes.c_void_p
+_DTYPE_CODE = {torch.bfloat16: 0, torch.float32: 1, torch.float16: 2}
 
 
 @dataclass(frozen=True)
@@ -58,61 +61,13 @@ def available() -> bool:
         return False
 
 
-def quantize_w4(w: torch.Tensor, group: int = GROUP,
-                clip_grid: tuple[float, ...] | None = None
-                ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """[N, K] -> (q uint8 0..15 [N, K], scale bf16 [N, K/group], zero int16 [N, K/group]).
-
-    Per (row, group) and clip fraction c of the min/max half-range: scale = bf16((hi_c - lo_c)
-    / 15); a constant nonzero group gets scale bf16(|lo| / 7) and zero 8; zero = round(-lo_c /
-    scale) clamped to +-1024; q = clamp(round(w / scale + zero), 0, 15); the c with the least
-    squared error wins (ties keep the earlier c). Float32 arithmetic throughout."""
-    n, k = w.shape
-    assert k % group == 0, f"K={k} must be a multiple of the group {group}"
-    wf = w.float().reshape(n, k // group, group)
-    lo, hi = wf.amin(-1), wf.amax(-1)
-    mid, half = (hi + lo) / 2, (hi - lo) / 2
-    best_err = torch.full_like(lo, float("inf"))
-    best_scale = torch.zeros_like(lo)
-    best_zero = torch.zeros_like(lo)
-    for c in (clip_grid if clip_grid is not None else CLIP_GRID):
-        lo_c, hi_c = mid - c * half, mid + c * half
-        scale = ((hi_c - lo_c) / 15.0).clamp(min=0.0).to(torch.bfloat16).float()
-        flat = (scale == 0) & (lo != 0)
-        scale = torch.where(flat, (lo.abs() / 7.0).to(torch.bfloat16).float(), scale)
-        inv = torch.where(scale > 0, 1.0 / scale.clamp(min=1e-30), torch.zeros_like(scale))
-        zero = torch.where(flat, torch.full_like(lo, 8.0),
-                           torch.round(-lo_c * inv)).clamp_(-1024, 1024)
-        q = torch.round(wf * inv.unsqueeze(-1) + zero.unsqueeze(-1)).clamp_(0, 15)
-        err = ((q - zero.unsqueeze(-1)) * scale.unsqueeze(-1) - wf).square().sum(-1)
-        take = err < best_err
-        best_err = torch.where(take, err, best_err)
-        best_scale = torch.where(take, scale, best_scale)
-        best_zero = torch.where(take, zero, best_zero)
-        del inv, zero, q, err
-    inv = torch.where(best_scale > 0, 1.0 / best_scale.clamp(min=1e-30),
-                      torch.zeros_like(best_scale))
-    q = torch.round(wf * inv.unsqueeze(-1) + best_zero.unsqueeze(-1)).clamp_(0, 15)
-    return (q.to(torch.uint8).reshape(n, k), best_scale.to(torch.bfloat16),
-            best_zero.to(torch.int16))
-
-
 # byte b of a lane's dword holds (low nibble, high nibble) = codes j of these pairs
 _LO = (0, 4, 1, 5)
 _HI = (2, 6, 3, 7)
 
 
-def pack_codes(q: torch.Tensor) -> torch.Tensor:
-    """[N, K] uint8 codes (N % 16 == 0) -> [N/16, K/128, 64, 16] in B-operand order."""
-    n, k = q.shape
-    v = q.reshape(n // 16, 16, k // 128, 4, 4, 8).permute(0, 2, 4, 1, 3, 5)  # nt g c r i j
-    lo = v[..., list(_LO)]
-    hi = v[..., list(_HI)]
-    return (lo | (hi << 4)).contiguous().reshape(n // 16, k // 128, 64, 16)
-
-
 def unpack_codes(wq: torch.Tensor) -> torch.Tensor:
-    """Inverse of pack_codes -> [N, K] uint8."""
+    """Packed codes [N/16, K/128, 64, 16] -> [N, K] uint8."""
     nt, g = wq.shape[0], wq.shape[1]
     b = wq.reshape(nt, g, 4, 16, 4, 4)                    # nt g c r i byte
     q = torch.empty(nt, g, 4, 16, 4, 8, dtype=torch.uint8, device=wq.device)
@@ -120,14 +75,6 @@ def unpack_codes(wq: torch.Tensor) -> torch.Tensor:
         q[..., _LO[byte]] = b[..., byte] & 0xF
         q[..., _HI[byte]] = b[..., byte] >> 4
     return q.permute(0, 3, 1, 4, 2, 5).reshape(nt * 16, g * 128)   # nt r g i c j
-
-
-def pack_sz(scale: torch.Tensor, zero: torch.Tensor) -> torch.Tensor:
-    """(bf16 scale, int16 zero) [N, G] -> int32 [N/16, G, 16]."""
-    n, g = scale.shape
-    sb = scale.contiguous().view(torch.int16).to(torch.int32) & 0xFFFF
-    zb = zero.to(torch.int32) << 16
-    return (sb | zb).reshape(n // 16, 16, g).permute(0, 2, 1).contiguous()
 
 
 def unpack_sz(sz: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
@@ -141,30 +88,40 @@ def unpack_sz(sz: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     return scale, zero
 
 
-def pack_w4a16(weight: torch.Tensor, group: int = GROUP, chunk_tiles: int = 512,
-               clip_grid: tuple[float, ...] | None = None) -> PackedW4:
-    """[N, K] bf16/f32 lm_head weight -> PackedW4. Runs once at load, in chunks of
-    chunk_tiles 16-row tiles so the float32 temporaries stay small."""
+def pack_w4a16(weight: torch.Tensor, group: int = GROUP) -> PackedW4:
+    """[N, K] bf16 / f32 / f16 lm_head weight on the GPU -> PackedW4, one kernel launch
+    (rlu_pack_w4). Runs once at load; the result is what gemm_w4a16 reads."""
     assert weight.dim() == 2, f"expected [N, K], got {tuple(weight.shape)}"
     assert group == GROUP, "the kernel's group is 128"
+    if not weight.is_cuda:
+        raise ValueError("pack_w4a16 packs on the GPU: move the weight to the device first")
+    if weight.dtype not in _DTYPE_CODE:
+        raise TypeError(f"pack_w4a16 takes bf16, f32 or f16 weights, not {weight.dtype}")
     n, k = weight.shape
     if k % group:
         raise ValueError(f"K={k} must be a multiple of {group}")
+    if weight.stride(1) != 1:
+        weight = weight.contiguous()
     n_pad = (n + N_ALIGN - 1) // N_ALIGN * N_ALIGN
     dev = weight.device
     wq = torch.empty((n_pad // 16, k // group, 64, 16), dtype=torch.uint8, device=dev)
     sz = torch.empty((n_pad // 16, k // group, 16), dtype=torch.int32, device=dev)
-    rows = chunk_tiles * 16
-    for r0 in range(0, n_pad, rows):
-        r1 = min(r0 + rows, n_pad)
-        w = weight[r0:min(r1, n)]
-        if w.shape[0] < r1 - r0:
-            w = torch.cat([w, w.new_zeros(r1 - r0 - w.shape[0], k)], 0)
-        q, scale, zero = quantize_w4(w, group, clip_grid)
-        wq[r0 // 16:r1 // 16] = pack_codes(q)
-        sz[r0 // 16:r1 // 16] = pack_sz(scale, zero)
-        del q, scale, zero, w
+    with torch.cuda.device(dev):
+        rc = lib().rlu_pack_w4(_P(weight.data_ptr()), _DTYPE_CODE[weight.dtype],
+                               weight.stride(0), n, k, n_pad, _P(wq.data_ptr()),
+                               _P(sz.data_ptr()), _P(stream_ptr()))
+    check(rc, "rlu_pack_w4")
     return PackedW4(wq=wq, sz=sz, n=n, n_pad=n_pad, k=k)
+
+
+def quantize_w4(w: torch.Tensor, group: int = GROUP
+                ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """[N, K] -> (q uint8 0..15 [N, K], scale bf16 [N, K/group], zero int16 [N, K/group]):
+    the codes pack_w4a16 stores, read back out of the packed layout."""
+    p = pack_w4a16(w, group)
+    scale, zero = unpack_sz(p.sz)
+    return (unpack_codes(p.wq)[:p.n], scale[:p.n].to(torch.bfloat16),
+            zero[:p.n].to(torch.int16))
 
 
 def unpack_w4(packed: PackedW4, dtype: torch.dtype = torch.float32) -> torch.Tensor:
@@ -176,19 +133,60 @@ def unpack_w4(packed: PackedW4, dtype: torch.dtype = torch.float32) -> torch.Ten
     return w.reshape(packed.n_pad, packed.k)[:packed.n].to(dtype)
 
 
-def gemm_w4a16(x: torch.Tensor, packed: PackedW4, out: torch.Tensor | None = None,
-               wv: int = 0) -> torch.Tensor:
-    """[M, K] bf16 hidden states -> [M, N] bf16 logits. No host sync, no allocation besides
-    the output (none when `out` [M, N_pad] is given), so it can be captured in a HIP graph."""
-    assert x.dim() == 2 and x.shape[1] == packed.k, f"expected [*, {packed.k}], got {tuple(x.shape)}"
-    x = x.to(torch.bfloat16).contiguous()
+def _gemm_into(x: torch.Tensor, packed_wq: torch.Tensor, packed_sz: torch.Tensor, k: int,
+               y: torch.Tensor, wv: int) -> None:
     m = x.shape[0]
-    y = torch.empty((m, packed.n_pad), dtype=torch.bfloat16, device=x.device) if out is None else out
-    assert y.shape == (m, packed.n_pad) and y.is_contiguous()
+    n_pad = packed_wq.shape[0] * 16
     for r0 in range(0, m, MAX_M):
         r1 = min(m, r0 + MAX_M)
-        rc = lib().rlu_gemm_w4_m16(_P(x[r0:r1].data_ptr()), r1 - r0, packed.k,
-                                   _P(packed.wq.data_ptr()), _P(packed.sz.data_ptr()),
-                                   _P(y[r0:r1].data_ptr()), packed.n_pad, wv, _P(stream_ptr()))
+        rc = lib().rlu_gemm_w4_m16(_P(x[r0:r1].data_ptr()), r1 - r0, k,
+                                   _P(packed_wq.data_ptr()), _P(packed_sz.data_ptr()),
+                                   _P(y[r0:r1].data_ptr()), n_pad, wv, _P(stream_ptr()))
         check(rc, "rlu_gemm_w4_m16")
-    return y if packed.n_pad == packed.n else y[:, :packed.n]
+
+
+def _draft_w4_lmhead_gemm(x: torch.Tensor, wq: torch.Tensor, wsz: torch.Tensor, n: int,
+                          k: int, wv: int, sk: int, npw: int, nt: int) -> torch.Tensor:
+    """The op of kernels/draft_w4_lmhead.py:351-390: [M, K] hidden states -> [M, n] bf16
+    logits, every M in one opaque call (16-row slices inside). wv = workgroups per CU of the
+    kernel's persistent grid (0: the kernel's default). sk / npw / nt name the closed kernel's
+    K split, columns per wave and tile shape; this kernel derives its K split from K and has one
+    item shape, so they are accepted for the schema (non-negative) and not used."""
+    if min(wv, sk, npw, nt) < 0:
+        raise ValueError("draft_w4_lmhead_gemm: negative config")
+    assert x.dim() == 2 and x.shape[1] == k, f"expected [*, {k}], got {tuple(x.shape)}"
+    x = x.to(torch.bfloat16).contiguous()
+    n_pad = wq.shape[0] * 16
+    y = torch.empty((x.shape[0], n_pad), dtype=torch.bfloat16, device=x.device)
+    _gemm_into(x, wq, wsz, k, y, wv)
+    return y if n_pad == n else y[:, :n].contiguous()
+
+
+def _register():
+    from .lru import OPS_NAMESPACE
+    lib_ = torch.library.Library(OPS_NAMESPACE, "FRAGMENT")
+    lib_.define("draft_w4_lmhead_gemm(Tensor x, Tensor wq, Tensor wsz, int n, int k, int wv, "
+                "int sk, int npw, int nt) -> Tensor")
+    lib_.impl("draft_w4_lmhead_gemm", _draft_w4_lmhead_gemm, "CUDA")
+    lib_.impl("draft_w4_lmhead_gemm",
+              lambda x, wq, wsz, n, *a: torch.empty((x.shape[0], n), dtype=torch.bfloat16,
+                                                    device=x.device), "Meta")
+    return lib_
+
+
+_OPS_LIB = _register()
+
+
+def gemm_w4a16(x: torch.Tensor, packed: PackedW4, out: torch.Tensor | None = None,
+               wv: int = 0) -> torch.Tensor:
+    """[M, K] bf16 hidden states -> [M, N] bf16 logits through the draft_w4_lmhead_gemm op
+    (kernels/draft_w4_lmhead.py:393-403). With `out` ([M, N_pad] bf16) the kernel writes into
+    it and nothing is allocated, for callers that capture it into a HIP graph."""
+    assert x.dim() == 2 and x.shape[1] == packed.k, f"expected [*, {packed.k}], got {tuple(x.shape)}"
+    if out is None:
+        op = getattr(torch.ops, OPS_NS).draft_w4_lmhead_gemm
+        return op(x, packed.wq, packed.sz, packed.n, packed.k, wv, 0, 0, 0)
+    x = x.to(torch.bfloat16).contiguous()
+    assert out.shape == (x.shape[0], packed.n_pad) and out.is_contiguous()
+    _gemm_into(x, packed.wq, packed.sz, packed.k, out, wv)
+    return out if packed.n_pad == packed.n else out[:, :packed.n]

@@ -47,6 +47,7 @@ def test_bad_arguments_return_minus_one_without_launching(pkg):
     assert lib.r4d_lru_manage(P(0), 0, 8, 1025, 1, 1, *z, P(0)) == -1       # S > 1024
     assert lib.r4d_lru_manage(P(0), 0, 8, 4, 1, 1025, *z, P(0)) == -1       # maxi > 1024
     assert lib.r4d_lru_manage(P(0), 0, 8, 4, 1, -1, *z, P(0)) == -1         # maxi < 0
+    assert lib.r4d_lru_manage(P(0), 0, 1025, 4, 1, 1, *z, P(0)) == -1       # E > 1024
     o = [P(0)] * 6
     assert lib.r4d_lru_fused(P(0), 10, 1025, 4, 1, 1, *z, 16, 10, 1, *o, P(0)) == -1
     assert lib.r4d_lru_fused(P(0), 10, 8, 4, 1, 1, *z, 0, 10, 1, *o, P(0)) == -1
@@ -57,6 +58,17 @@ def test_bad_arguments_return_minus_one_without_launching(pkg):
     assert lib.r4d_lru_gather(*g_bad, P(0), P(0), 8, 16, P(0)) == -1
     assert lib.r4d_lru_gather(*g, P(0), P(0), 0, 16, P(0)) == -1
     assert lib.r4d_lru_gather(*g, P(0), P(0), 8, 0, P(0)) == -1
+    pk = lib.rlu_pack_w4
+    assert pk(P(0), 0, 256, 16, 256, 16, P(0), P(0), P(0)) == -1            # null pointers
+    a = P(4096)
+    assert pk(a, 0, 256, 0, 256, 16, a, a, P(0)) == -1                      # N < 1
+    assert pk(a, 0, 256, 32, 256, 16, a, a, P(0)) == -1                     # n_pad < N
+    assert pk(a, 0, 100, 16, 128, 16, a, a, P(0)) == -1                     # ld < K
+    assert pk(a, 0, 200, 16, 200, 16, a, a, P(0)) == -2                     # K % 128
+    assert pk(a, 0, 256, 16, 256, 24, a, a, P(0)) == -2                     # n_pad % 16
+    assert pk(a, 3, 256, 16, 256, 16, a, a, P(0)) == -3                     # dtype
+    assert pk(a, 0, 260, 16, 256, 16, a, a, P(0)) == -4                     # row alignment
+    assert pk(P(4098), 0, 256, 16, 256, 16, a, a, P(0)) == -4               # base alignment
 
 
 def test_missing_library_fails_loudly(pkg, monkeypatch, tmp_path):

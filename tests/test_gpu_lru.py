@@ -645,3 +645,22 @@ def test_multilayer_graph_fused_and_gather(pkg, mine):
         total += check(n, f"replay {n}")
     assert total > 0, "the traces must insert"
     del gr
+
+
+def test_manage_negative_mk_is_no_tokens(mine, ref):
+    """kernels/lru/r4d_lru.hip:583-587 launches for any mk; its loops over mk ids then run zero
+    times: step advances, n_miss = 0, nothing else changes. The same here, side by side."""
+    ids, s = victim_case(E=512, S=257, mk=50, k_cold=5, maxi=64, seed=4)
+    want = s.copy()
+    olru.manage(want, np.zeros(0, np.int32))
+    ids_t = torch.from_numpy(ids.astype(np.int32)).to(DEV)
+    for libh, tag in ((mine, "mine"), (ref, "ref")):
+        d = to_dev(s)
+        args = [ctypes.c_void_p(d[n].data_ptr()) for n in NAMES]
+        gpu_case(f"manage mk=-5 ({tag})")
+        rc = libh.r4d_lru_manage(ctypes.c_void_p(ids_t.data_ptr()), -5, 512, 257,
+                                 s.max_distinct, s.max_inserts, *args,
+                                 ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        assert rc == 0
+        torch.cuda.synchronize()
+        assert_state(d, want, f"mk<0 {tag}")

@@ -641,3 +641,96 @@ def test_fp8_target_head_packs_its_weight(ops):
     torch.cuda.synchronize()
     assert torch.equal(head.wq.view(torch.uint8), wt.view(torch.uint8))
     assert torch.equal(head.ws, ws)
+
+
+# ---- the grouped-GEMM torch ops at the reference's names ---------------------------------------
+def _c_gemm(pkg, y, qx, xs, wq_ptr, ws_ptr, al, tw, mtk, top_k, npw=4, sk=0):
+    """The C-ABI call itself (r4d_gemm_moe_fp8blk_nt_b16), no Python op in between."""
+    P = ctypes.c_void_p
+    rc = pkg.lib().r4d_gemm_moe_fp8blk_nt_b16(
+        P(qx.data_ptr()), P(xs.data_ptr()), P(wq_ptr), P(ws_ptr), P(0), P(y.data_ptr()),
+        P(al[0].data_ptr()), P(al[1].data_ptr()), P(al[2].data_ptr()),
+        P(0 if tw is None else tw.data_ptr()), al[0].numel(), mtk, top_k, qx.shape[1],
+        y.shape[1], 0, sk, npw, P(torch.cuda.current_stream().cuda_stream))
+    assert rc == 0
+
+
+def test_moe_gemm_ops_equal_c_abi(pkg, ops, layer):
+    """torch.ops.<ns>.r4d_mxfp4_moe_gemm_into (patches/.../r4d_mxfp4_moe.py.lru.diff:363-423,
+    mutates y) over the hot slots and then the full expert tensor in pinned host memory, and
+    the allocating r4d_mxfp4_moe_gemm (:625,635) over one all-expert align, equal the C-ABI
+    calls bit for bit -- eagerly, and replayed three times from a captured graph with new
+    activations and routed weights."""
+    ns = getattr(torch.ops, pkg.lru.OPS_NAMESPACE)
+    E, H, I = layer["E"], layer["H"], layer["I"]
+    M, top_k = 5, 10
+    ids = routing(M, top_k, E, seed=51)
+    mtk = ids.size
+    hot_experts = sorted(set(ids.reshape(-1).tolist()))[::3]
+    hot = {ex: i for i, ex in enumerate(hot_experts)}
+    al = to_dev_i32(*align_all(ids, E, hot))
+    al_all = to_dev_i32(*align_all(ids, E))
+    idx = torch.tensor(hot_experts, device=DEV)
+    sq, ss = layer["w2t"][idx].contiguous(), layer["w2s"][idx].contiguous()
+    hq = torch.empty(layer["w2t"].shape, dtype=layer["w2t"].dtype, pin_memory=True)
+    hs = torch.empty(layer["w2s"].shape, dtype=torch.float32, pin_memory=True)
+    hq.copy_(layer["w2t"])
+    hs.copy_(layer["w2s"])
+    hqp, hsp = pkg._lib.device_ptr_of_pinned(hq), pkg._lib.device_ptr_of_pinned(hs)
+    rng = np.random.default_rng(5)
+
+    def inputs():
+        x = fp8.bf16_round(rng.standard_normal((mtk, I)).astype(np.float32))
+        q, s_ = fp8.group_quant(x, 128)
+        return (torch.from_numpy(q).to(DEV).view(torch.float8_e4m3fn),
+                torch.from_numpy(s_).to(DEV),
+                torch.from_numpy(rng.random(mtk).astype(np.float32)).to(DEV))
+
+    def expected(q, s_, tw):
+        yc = torch.full((mtk, H), float("nan"), dtype=torch.bfloat16, device=DEV)
+        _c_gemm(pkg, yc, q, s_, sq.data_ptr(), ss.data_ptr(), al[0:3], tw, mtk, 1)
+        _c_gemm(pkg, yc, q, s_, hqp, hsp, al[3:6], tw, mtk, 1)
+        ya = torch.full((mtk, H), float("nan"), dtype=torch.bfloat16, device=DEV)
+        _c_gemm(pkg, ya, q, s_, layer["w2t"].data_ptr(), layer["w2s"].data_ptr(), al_all, tw,
+                mtk, 1)
+        return yc, ya
+
+    q, s_, tw = inputs()
+    y = torch.full((mtk, H), float("nan"), dtype=torch.bfloat16, device=DEV)
+    gpu_case("gemm ops eager")
+    ns.r4d_mxfp4_moe_gemm_into(y, q, s_, sq, ss, None, *al[0:3], tw, mtk, 1, 0, 0, 4)
+    ns.r4d_mxfp4_moe_gemm_into(y, q, s_, hq, hs, None, *al[3:6], tw, mtk, 1, 0, 0, 4)
+    ya = ns.r4d_mxfp4_moe_gemm(q, s_, layer["w2t"], layer["w2s"], None, *al_all, tw, mtk, 1,
+                               0, 0, 4)
+    yc, yac = expected(q, s_, tw)
+    torch.cuda.synchronize()
+    assert not torch.isnan(y).any() and ya.shape == (mtk, H)
+    assert torch.equal(y.view(torch.int16), yc.view(torch.int16))
+    assert torch.equal(ya.view(torch.int16), yac.view(torch.int16))
+    assert torch.equal(y.view(torch.int16), ya.view(torch.int16))    # partition invariance
+
+    qg, sg, twg = q.clone(), s_.clone(), tw.clone()
+    yg = torch.empty_like(y)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        ns.r4d_mxfp4_moe_gemm_into(yg, qg, sg, sq, ss, None, *al[0:3], twg, mtk, 1, 0, 0, 4)
+    torch.cuda.current_stream().wait_stream(side)
+    gr = torch.cuda.CUDAGraph()
+    gpu_case("gemm ops graph capture")
+    with torch.cuda.graph(gr):
+        ns.r4d_mxfp4_moe_gemm_into(yg, qg, sg, sq, ss, None, *al[0:3], twg, mtk, 1, 0, 0, 4)
+        ns.r4d_mxfp4_moe_gemm_into(yg, qg, sg, hq, hs, None, *al[3:6], twg, mtk, 1, 0, 0, 4)
+        yag = ns.r4d_mxfp4_moe_gemm(qg, sg, layer["w2t"], layer["w2s"], None, *al_all, twg,
+                                    mtk, 1, 0, 0, 4)
+    for _ in range(3):
+        q, s_, tw = inputs()
+        qg.copy_(q)
+        sg.copy_(s_)
+        twg.copy_(tw)
+        gr.replay()
+        torch.cuda.synchronize()
+        yc, yac = expected(q, s_, tw)
+        torch.cuda.synchronize()
+        assert torch.equal(yg.view(torch.int16), yc.view(torch.int16))
+        assert torch.equal(yag.view(torch.int16), yac.view(torch.int16))

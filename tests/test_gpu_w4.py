@@ -5,8 +5,12 @@
   at vocab 151936 x 2560 for M in {1, 4, 8}, plus M = 16 and the 16-row chunking at M = 20;
 * small and edge shapes: N not a multiple of 16 (zero-row padding), K = 4096 (the LDS limit),
   M = 1 with one strip;
-* the GPU packer equals the CPU packer (codes, scales, zeros), up to float32 clip ties;
-* HIP-graph replay equals eager; bad arguments return codes.
+* the packing kernel (rlu_pack_w4) writes the oracle's bytes exactly -- codes, scales and
+  zeros -- for bf16 / f32 / f16 weights, N not a multiple of 16 or 32, K up to 4096, special
+  groups (zero, constant, one-sided, offset past the zero range), and on sampled strips of the
+  151936 x 2560 head;
+* the draft_w4_lmhead_gemm op (torch.ops) equals the C-ABI call bit for bit, eagerly and
+  inside a captured graph; HIP-graph replay equals eager; bad arguments return codes.
 """
 from __future__ import annotations
 
@@ -91,19 +95,109 @@ def test_w4_shapes(pw4, N, K, M):
     assert rel(y.float().cpu().numpy(), ref_logits(packed, x)) <= TOL
 
 
-def test_w4_gpu_packer_equals_cpu(pw4):
-    g = torch.Generator().manual_seed(11)
-    w = torch.randn(256, 1024, generator=g) * 0.02
-    gpu_case("w4 packer gpu vs cpu")
-    pg = pw4.pack_w4a16(w.to(DEV))
-    pc = pw4.pack_w4a16(w)
-    sg, sc = pg.sz.cpu().numpy(), pc.sz.numpy()
-    same = sg == sc
-    assert same.mean() > 0.999
-    qg = pw4.unpack_codes(pg.wq.cpu()).numpy().reshape(256, 8, 128)
-    qc = pw4.unpack_codes(pc.wq).numpy().reshape(256, 8, 128)
-    nt, gg, r = np.nonzero(same)
-    assert np.array_equal(qg[nt * 16 + r, gg], qc[nt * 16 + r, gg])
+def _oracle_bytes(w32: np.ndarray, n_pad: int):
+    n, k = w32.shape
+    wp = np.zeros((n_pad, k), np.float32)
+    wp[:n] = w32
+    q, s, z = ow4.quantize_w4(wp)
+    return ow4.pack_codes(q), ow4.pack_sz(s, z)
+
+
+def _special_weight(N, K, seed):
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    w[0, :128] = 0.0                                  # all zero
+    w[1, :128] = 0.75                                 # constant positive
+    w[2, 128:256] = -0.3                              # constant negative
+    w[3, :128] = np.linspace(0.5, 1.0, 128)           # one-sided
+    w[4, :128] = np.linspace(100.0, 100.01, 128)      # offset past the zero range
+    w[5, :] = rng.standard_t(2, K) * 0.05             # heavy tails
+    return w
+
+
+@pytest.mark.parametrize("N,K,dtype", [(256, 1024, torch.float32), (40, 256, torch.bfloat16),
+                                       (37, 128, torch.float16), (1000, 4096, torch.bfloat16),
+                                       (96, 2560, torch.float32)])
+def test_w4_packer_bit_exact_vs_oracle(pw4, N, K, dtype):
+    w = torch.from_numpy(_special_weight(N, K, N + K)).to(dtype)
+    w32 = w.float().numpy()                 # the values the kernel reads
+    gpu_case(f"w4 pack N={N} K={K} {dtype}")
+    p = pw4.pack_w4a16(w.to(DEV))
+    torch.cuda.synchronize()
+    wq, sz = _oracle_bytes(w32, p.n_pad)
+    assert np.array_equal(p.wq.cpu().numpy(), wq)
+    assert np.array_equal(p.sz.cpu().numpy(), sz)
+    q, s, z = pw4.quantize_w4(w.to(DEV))
+    q0, s0, z0 = ow4.quantize_w4(w32)
+    assert np.array_equal(q.cpu().numpy(), q0)
+    assert np.array_equal(s.float().cpu().numpy(), s0) and np.array_equal(z.cpu().numpy(), z0)
+
+
+def test_w4_packer_bit_exact_on_the_head(pw4, big):
+    """The 151936 x 2560 head packed once (the `big` fixture, f32 weights from seed 5): 64
+    sampled 16-row strips, re-quantized by the oracle, match byte for byte."""
+    packed, _ = big
+    N, K = 151936, 2560
+    g = torch.Generator(device=DEV).manual_seed(5)
+    w = torch.randn(N, K, device=DEV, generator=g) * 0.02
+    strips = np.random.default_rng(1).choice(N // 16, 64, replace=False)
+    rows = (strips[:, None] * 16 + np.arange(16)[None, :]).reshape(-1)
+    w32 = w[torch.from_numpy(rows).to(DEV)].cpu().numpy()
+    del w
+    q, s, z = ow4.quantize_w4(w32)
+    wq = ow4.pack_codes(q).reshape(64, K // 128, 64, 16)
+    sz = ow4.pack_sz(s, z).reshape(64, K // 128, 16)
+    idx = torch.from_numpy(strips).to(DEV)
+    assert np.array_equal(packed.wq[idx].cpu().numpy(), wq)
+    assert np.array_equal(packed.sz[idx].cpu().numpy(), sz)
+
+
+def test_w4_packer_deterministic(pw4):
+    g = torch.Generator(device=DEV).manual_seed(2)
+    w = torch.randn(4096, 2560, device=DEV, generator=g).to(torch.bfloat16) * 0.02
+    a, b = pw4.pack_w4a16(w), pw4.pack_w4a16(w)
+    torch.cuda.synchronize()
+    assert torch.equal(a.wq, b.wq) and torch.equal(a.sz, b.sz)
+
+
+def test_w4_op_equals_c_abi(pw4, pkg):
+    """torch.ops.<ns>.draft_w4_lmhead_gemm (kernels/draft_w4_lmhead.py:351-390) equals the
+    C-ABI call bit for bit, eagerly and replayed from a captured graph; M > 16 and N not a
+    multiple of 32 go through the same op."""
+    op = getattr(torch.ops, pkg.lru.OPS_NAMESPACE).draft_w4_lmhead_gemm
+    g = torch.Generator(device=DEV).manual_seed(4)
+    packed = pw4.pack_w4a16(torch.randn(2000, 2560, device=DEV, generator=g) * 0.02)
+    for M in (1, 5, 20):
+        x = torch.randn(M, 2560, device=DEV, generator=g).to(torch.bfloat16)
+        gpu_case(f"w4 op eager M={M}")
+        y_op = op(x, packed.wq, packed.sz, packed.n, packed.k, 0, 0, 0, 0)
+        y_c = torch.empty((M, packed.n_pad), dtype=torch.bfloat16, device=DEV)
+        pw4._gemm_into(x, packed.wq, packed.sz, packed.k, y_c, 0)
+        torch.cuda.synchronize()
+        assert y_op.shape == (M, 2000) and y_op.is_contiguous()
+        assert torch.equal(y_op.view(torch.int16), y_c[:, :2000].view(torch.int16))
+    M = 4
+    xs = [torch.randn(M, 2560, device=DEV, generator=g).to(torch.bfloat16) for _ in range(3)]
+    x = xs[0].clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        op(x, packed.wq, packed.sz, packed.n, packed.k, 0, 0, 0, 0)
+    torch.cuda.current_stream().wait_stream(side)
+    gr = torch.cuda.CUDAGraph()
+    gpu_case("w4 op graph capture")
+    with torch.cuda.graph(gr):
+        y = op(x, packed.wq, packed.sz, packed.n, packed.k, 0, 0, 0, 0)
+    for xi in xs:
+        x.copy_(xi)
+        gr.replay()
+        torch.cuda.synchronize()
+        y_c = torch.empty((M, packed.n_pad), dtype=torch.bfloat16, device=DEV)
+        pw4._gemm_into(xi, packed.wq, packed.sz, packed.k, y_c, 0)
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), y_c[:, :2000].view(torch.int16))
+    with pytest.raises(ValueError):
+        op(x, packed.wq, packed.sz, packed.n, packed.k, -1, 0, 0, 0)
 
 
 def test_w4_graph_replay(pw4):
