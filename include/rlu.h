@@ -180,6 +180,24 @@ int rlu_moe_gemm_fp8blk_tiled(const void* qx, const float* xs, const void* wq, c
                               void* y, int mtk, int top_k, int K, int N, int wv,
                               hipStream_t stream);
 
+/* No counterpart in the reference. For callers that cannot allocate -- code recorded into a HIP
+ * graph, serving loops and harnesses that forbid hipMalloc: rlu_moe_gemm_tiles followed by
+ * rlu_moe_gemm_fp8blk_tiled (same kernels, same results bit for bit) with the tile list kept in
+ * this library's own per-device scratch array (64 KB of device memory per GPU, held until the
+ * process ends) instead of a caller workspace. Nothing is allocated, nothing is freed. nb =
+ * the align output's block count (expert_ids holds nb entries), at most 8192 (131072 sorted
+ * ids): larger returns -7 and launches nothing. The scratch address is looked up once per
+ * device, on the first call with that device current -- make that first call outside graph
+ * capture. Every call on one GPU shares its scratch (each call rewrites all it reads), so
+ * calls that overlap on one GPU -- concurrent streams, or graphs replayed concurrently -- race;
+ * calls in stream order do not. Returns -1 / -2 / -5 as rlu_moe_gemm_fp8blk_tiled, -7 nb >
+ * 8192, or a HIP error code. */
+int rlu_moe_gemm_fp8blk_tiled_noalloc(const void* qx, const float* xs, const void* wq,
+                                      const float* ws, const int* sorted_ids,
+                                      const int* expert_ids, const int* num_post_pad, int nb,
+                                      const float* topk_weights, void* y, int mtk, int top_k,
+                                      int K, int N, int wv, hipStream_t stream);
+
 /* Replaces the closed r4d_gemm_w4a16_nt_m64 behind draft_w4_lmhead_gemm / gemm_w4a16
  * (kernels/draft_w4_lmhead.py:351-403), in this build's gfx950 W4 format:
  *   y [M, N] bf16 = x [M, K] bf16 . (scale * (q - zero))^T, 1 <= M <= 16,

@@ -17,6 +17,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "gemm_common.h"
 #include "numerics.h"
 #include "rlu.h"
@@ -236,6 +238,62 @@ __global__ __launch_bounds__(NTHR) void tiled_k(const uint8_t* __restrict__ qx,
   }
 }
 
+// ---- the no-allocation entry's workspace -----------------------------------------------------
+// The tile list of one call: 2 ints per tile (at most one tile per block) and the count, for up
+// to MAXNB blocks -- 64 KB per GPU, held until the process ends. Host code never uses the
+// array's name as an address: each device's address comes from hipGetSymbolAddress, taken once
+// per device with that device current, and only that pointer reaches the kernels.
+constexpr int SCRATCH_INTS = 2 * MAXNB + 64;
+static __device__ __align__(256) int scratch[SCRATCH_INTS];
+
+constexpr int MAXDEV = 64;
+static std::mutex scratch_mu;
+static int* scratch_dev[MAXDEV];
+
+// this device's scratch address; 0 or a HIP error code
+static int scratch_ptr(int** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= MAXDEV) return (int)hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (!scratch_dev[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (!p) return (int)hipErrorInvalidSymbol;
+    scratch_dev[dev] = static_cast<int*>(p);
+  }
+  *out = scratch_dev[dev];
+  return 0;
+}
+
+static int check_gemm_args(int mtk, int top_k, int K, int N, int max_tiles, int wv) {
+  if (mtk < 0 || top_k < 1 || K <= 0 || N <= 0 || max_tiles <= 0) return -1;
+  if (K % 128 || N % TBN) return -2;
+  if (wv < 0 || wv > 16) return -5;
+  return 0;
+}
+
+static void launch_tiled(const void* qx, const float* xs, const void* wq, const float* ws,
+                         const int* sorted_ids, const int* expert_ids, const int* tiles,
+                         const int* ntiles, int max_tiles, const float* topk_weights, void* y,
+                         int mtk, int top_k, int K, int N, int wv, hipStream_t stream) {
+  const int items = max_tiles * (N / TBN);
+  int grid = rlu::device_cus() * (wv ? wv : 2);
+  if (grid > items) grid = items;
+  if (grid >= NXCD) grid -= grid % NXCD;           // whole XCD rounds (see tiled_k)
+  const size_t lds = sizeof(Smem);
+  if (topk_weights)
+    hipLaunchKernelGGL(tiled_k<true>, dim3(grid), dim3(NTHR), lds, stream, (const uint8_t*)qx,
+                       xs, (const uint8_t*)wq, ws, sorted_ids, expert_ids, tiles, ntiles,
+                       (uint16_t*)y, topk_weights, mtk, top_k, K, N);
+  else
+    hipLaunchKernelGGL(tiled_k<false>, dim3(grid), dim3(NTHR), lds, stream, (const uint8_t*)qx,
+                       xs, (const uint8_t*)wq, ws, sorted_ids, expert_ids, tiles, ntiles,
+                       (uint16_t*)y, nullptr, mtk, top_k, K, N);
+}
+
 }  // namespace tiled
 }  // namespace rlu
 
@@ -257,23 +315,35 @@ int rlu_moe_gemm_fp8blk_tiled(const void* qx, const float* xs, const void* wq, c
                               void* y, int mtk, int top_k, int K, int N, int wv,
                               hipStream_t stream) {
   using namespace rlu::tiled;
-  if (mtk < 0 || top_k < 1 || K <= 0 || N <= 0 || max_tiles <= 0) return -1;
-  if (K % 128 || N % TBN) return -2;
-  if (wv < 0 || wv > 16) return -5;
+  const int rc = check_gemm_args(mtk, top_k, K, N, max_tiles, wv);
+  if (rc) return rc;
   if (mtk == 0) return 0;
-  const int items = max_tiles * (N / TBN);
-  int grid = rlu::device_cus() * (wv ? wv : 2);
-  if (grid > items) grid = items;
-  if (grid >= NXCD) grid -= grid % NXCD;           // whole XCD rounds (see tiled_k)
-  const size_t lds = sizeof(Smem);
-  if (topk_weights)
-    hipLaunchKernelGGL(tiled_k<true>, dim3(grid), dim3(NTHR), lds, stream, (const uint8_t*)qx,
-                       xs, (const uint8_t*)wq, ws, sorted_ids, expert_ids, tiles, ntiles,
-                       (uint16_t*)y, topk_weights, mtk, top_k, K, N);
-  else
-    hipLaunchKernelGGL(tiled_k<false>, dim3(grid), dim3(NTHR), lds, stream, (const uint8_t*)qx,
-                       xs, (const uint8_t*)wq, ws, sorted_ids, expert_ids, tiles, ntiles,
-                       (uint16_t*)y, nullptr, mtk, top_k, K, N);
+  launch_tiled(qx, xs, wq, ws, sorted_ids, expert_ids, tiles, ntiles, max_tiles, topk_weights, y,
+               mtk, top_k, K, N, wv, stream);
+  return (int)hipGetLastError();
+}
+
+// rlu_moe_gemm_tiles + rlu_moe_gemm_fp8blk_tiled with the tile list in this library's
+// per-device scratch array instead of a caller workspace: nothing is allocated.
+int rlu_moe_gemm_fp8blk_tiled_noalloc(const void* qx, const float* xs, const void* wq,
+                                      const float* ws, const int* sorted_ids,
+                                      const int* expert_ids, const int* num_post_pad, int nb,
+                                      const float* topk_weights, void* y, int mtk, int top_k,
+                                      int K, int N, int wv, hipStream_t stream) {
+  using namespace rlu::tiled;
+  if (!expert_ids || !num_post_pad) return -1;
+  const int rc = check_gemm_args(mtk, top_k, K, N, nb, wv);
+  if (rc) return rc;
+  if (nb > MAXNB) return -7;                        // beyond the scratch tile list
+  if (mtk == 0) return 0;
+  int* ws_tiles = nullptr;
+  const int e = scratch_ptr(&ws_tiles);
+  if (e) return e;
+  int* ws_count = ws_tiles + 2 * MAXNB;
+  hipLaunchKernelGGL(tiles_k, dim3(1), dim3(TB_THR), 0, stream, expert_ids, num_post_pad, nb,
+                     ws_tiles, ws_count);
+  launch_tiled(qx, xs, wq, ws, sorted_ids, expert_ids, ws_tiles, ws_count, nb, topk_weights, y,
+               mtk, top_k, K, N, wv, stream);
   return (int)hipGetLastError();
 }
 

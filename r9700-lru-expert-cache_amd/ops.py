@@ -248,6 +248,30 @@ def moe_gemm_tiled(y: torch.Tensor, qx: torch.Tensor, x_scale: torch.Tensor, wq:
     check(rc, "rlu_moe_gemm_fp8blk_tiled")
 
 
+NOALLOC_MAX_BLOCKS = 8192      # the scratch tile list's capacity (131072 sorted ids)
+
+
+def moe_gemm_tiled_noalloc(y: torch.Tensor, qx: torch.Tensor, x_scale: torch.Tensor,
+                           wq: torch.Tensor, ws_t: torch.Tensor, sorted_ids: torch.Tensor,
+                           expert_ids: torch.Tensor, num_post_pad: torch.Tensor,
+                           topk_weights: torch.Tensor | None, mtk: int, top_k: int,
+                           wv: int = 0) -> None:
+    """moe_gemm_tiled with no workspace and no allocation: the tile list lives in the
+    library's per-device scratch array. Calls that overlap on one GPU race on it."""
+    K = qx.shape[1]
+    N = wq.shape[1]
+    nb = expert_ids.numel()
+    assert y.shape == (mtk, N) and y.dtype == torch.bfloat16 and y.is_contiguous()
+    assert qx.dtype == FP8 and wq.dtype == FP8 and wq.shape[2] == K
+    if nb > NOALLOC_MAX_BLOCKS:
+        raise ValueError(f"moe_gemm_tiled_noalloc: {nb} blocks exceed the scratch tile list "
+                         f"({NOALLOC_MAX_BLOCKS} blocks)")
+    rc = lib().rlu_moe_gemm_fp8blk_tiled_noalloc(
+        _p(qx), _p(x_scale), _p(wq), _p(ws_t), _p(sorted_ids), _p(expert_ids), _p(num_post_pad),
+        nb, _p(topk_weights), _p(y), mtk, top_k, K, N, wv, _P(stream_ptr()))
+    check(rc, "rlu_moe_gemm_fp8blk_tiled_noalloc")
+
+
 # ---- torch custom ops at the reference's names and schemas ----------------------------------
 # r4d_mxfp4_moe_gemm_into / r4d_mxfp4_moe_gemm: patches/.../r4d_mxfp4_moe.py.lru.diff:363-423
 # (mutates_args=["y"], a fake impl) and the allocating call sites :625,635. Registered in the
