@@ -173,7 +173,12 @@ int rlu_moe_gemm_tiles(const int* expert_ids, const int* num_post_pad, int nb_ma
 /* Step 2: the same product, row contract and per-step accumulation as
  * r4d_gemm_moe_fp8blk_nt_b16 with sk = 1 (equal to it bit for bit), one workgroup per 128-row x
  * 256-column tile so an expert's weights are read once per tile. max_tiles bounds the device
- * count (the align output's block count). N % 256 == 0. Returns -1 / -2 / -5 as above. */
+ * count (the align output's block count). N % 256 == 0. wv = 0 picks the streamed kernel where
+ * one is built for K (K = 2560: gate_up of the 2560-wide model, K = 768: its down projection;
+ * persistent, one workgroup per CU walking (tile, 256-column strip) items with the weight stream
+ * kept in flight across items), else the general tiled kernel at 2 workgroups per CU; wv in
+ * 1..16 forces the general kernel at wv workgroups per CU. Every choice gives the same bits.
+ * Returns -1 / -2 / -5 as above. */
 int rlu_moe_gemm_fp8blk_tiled(const void* qx, const float* xs, const void* wq, const float* ws,
                               const int* sorted_ids, const int* expert_ids, const int* tiles,
                               const int* ntiles, int max_tiles, const float* topk_weights,

@@ -21,6 +21,7 @@
 
 #include "gemm_common.h"
 #include "numerics.h"
+#include "prefill.h"
 #include "rlu.h"
 #include "wave.h"
 
@@ -275,10 +276,16 @@ static int check_gemm_args(int mtk, int top_k, int K, int N, int max_tiles, int 
   return 0;
 }
 
+// The streamed kernel (prefill.hip) where K and N have a built configuration, tiled_k
+// otherwise; both give the same bits.
 static void launch_tiled(const void* qx, const float* xs, const void* wq, const float* ws,
                          const int* sorted_ids, const int* expert_ids, const int* tiles,
                          const int* ntiles, int max_tiles, const float* topk_weights, void* y,
                          int mtk, int top_k, int K, int N, int wv, hipStream_t stream) {
+  if (wv == 0 && rlu::launch_prefill_stream(qx, xs, wq, ws, sorted_ids, expert_ids, tiles,
+                                            ntiles, max_tiles, topk_weights, y, mtk, top_k, K,
+                                            N, stream) == 0)
+    return;
   const int items = max_tiles * (N / TBN);
   int grid = rlu::device_cus() * (wv ? wv : 2);
   if (grid > items) grid = items;

@@ -498,10 +498,13 @@ def test_moe_gemm_tile_list(ops, M, E_used):
     assert [tuple(x) for x in got[:2 * nt].reshape(-1, 2)] == want
 
 
+@pytest.mark.parametrize("wv", [0, 2])
 @pytest.mark.parametrize("M", [256, 600])
-def test_moe_gemm_tiled_equals_decode_kernel(ops, layer, M):
-    """Prefill-sized routing (64 / 150 rows per expert): the tiled kernel and the decode kernel
-    with sk = 1 run the same per-step fma sequence, so their outputs are bit-identical."""
+def test_moe_gemm_tiled_equals_decode_kernel(ops, layer, M, wv):
+    """Prefill-sized routing (64 / 150 rows per expert): the tiled kernels and the decode kernel
+    with sk = 1 run the same per-step fma sequence, so their outputs are bit-identical.
+    wv = 0 takes the streamed kernel (K = 2560 and 768 have one), wv = 2 the general tiled
+    kernel at two workgroups per CU."""
     E, H, I = layer["E"], layer["H"], layer["I"]
     top_k = 10
     ids = routing(M, top_k, E, seed=M + 1)
@@ -514,8 +517,9 @@ def test_moe_gemm_tiled_equals_decode_kernel(ops, layer, M):
     xs_t = torch.from_numpy(xs).to(DEV)
     yt = torch.full((mtk, 2 * I), float("nan"), dtype=torch.bfloat16, device=DEV)
     yd = torch.full_like(yt, float("nan"))
-    gpu_case(f"tiled gemm1 M={M}")
-    ops.moe_gemm_tiled(yt, qx_t, xs_t, layer["w13t"], layer["w13s"], *al, None, mtk, top_k)
+    gpu_case(f"tiled gemm1 M={M} wv={wv}")
+    ops.moe_gemm_tiled(yt, qx_t, xs_t, layer["w13t"], layer["w13s"], *al, None, mtk, top_k,
+                       wv=wv)
     run_gemm(ops, yd, qx_t, xs_t, layer["w13t"], layer["w13s"], al, None, mtk, top_k, npw=2, sk=1)
     torch.cuda.synchronize()
     assert not torch.isnan(yt).any()
@@ -528,8 +532,8 @@ def test_moe_gemm_tiled_equals_decode_kernel(ops, layer, M):
     tw = torch.from_numpy(rng.random(mtk).astype(np.float32)).to(DEV)
     zt = torch.full((mtk, H), float("nan"), dtype=torch.bfloat16, device=DEV)
     zd = torch.full_like(zt, float("nan"))
-    gpu_case(f"tiled gemm2 M={M}")
-    ops.moe_gemm_tiled(zt, q2_t, s2_t, layer["w2t"], layer["w2s"], *al, tw, mtk, 1)
+    gpu_case(f"tiled gemm2 M={M} wv={wv}")
+    ops.moe_gemm_tiled(zt, q2_t, s2_t, layer["w2t"], layer["w2s"], *al, tw, mtk, 1, wv=wv)
     run_gemm(ops, zd, q2_t, s2_t, layer["w2t"], layer["w2s"], al, tw, mtk, 1, npw=2, sk=1)
     torch.cuda.synchronize()
     assert not torch.isnan(zt).any()
