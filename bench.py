@@ -181,10 +181,9 @@ def gemm_launches(layers):
     """Both grouped GEMMs of every layer, eager, on the current stream (inputs as the last step
     left them)."""
     for L in layers:
-        L._gemm_split(L.ic1, L.qx, L.xs, L.slots.w13, L.slots.s13, L.full_ptrs[0],
-                      L.full_ptrs[1], None, L.top_k, L.npw1, L.sk1)
-        L._gemm_split(L.ic3, L.q2, L.s2, L.slots.w2, L.slots.s2, L.full_ptrs[2],
-                      L.full_ptrs[3], L.tw, 1, L.npw2, L.sk2)
+        L._gemm_split(L.ic1, L.qx, L.xs, L.slots.w13, L.slots.s13, 0, None, L.top_k, L.npw1,
+                      L.sk1)
+        L._gemm_split(L.ic3, L.q2, L.s2, L.slots.w2, L.slots.s2, 2, L.tw, 1, L.npw2, L.sk2)
 
 
 def load_traffic():

@@ -25,6 +25,9 @@ from .lru import LRU_CHUNKS, LRU_LANES, LruCache, _r4d_lru_gather, split_fresh
 
 _P = ctypes.c_void_p
 BLOCK = 16
+# Routed rows (tokens x top_k) from which a layer runs the tiled (prefill) grouped GEMM instead
+# of the decode one: a 2048-token chunk at top-10 gives 20480, ~40 rows per expert over 512.
+PREFILL_ROWS = 2048
 
 
 @dataclass
@@ -53,7 +56,8 @@ class LruMoELayer:
     def __init__(self, full: ExpertWeights, hot_ids, rank: dict | None, max_tokens: int,
                  top_k: int, device="cuda", slots: ExpertWeights | None = None,
                  npw1: int = 2, npw2: int = 4, sk1: int | None = None, sk2: int = 1,
-                 wv: int = 0, max_inserts: int | None = None):
+                 wv: int = 0, max_inserts: int | None = None,
+                 prefill_rows: int = PREFILL_ROWS):
         """npw / sk: 16-column tiles per item and K split of gate_up (1) and down (2); the
         defaults are the fastest measured at the decode shapes (hidden 2560, intermediate
         768): gate_up splits K over 2 waves above 8 tokens (20 tokens: 3.70 vs 3.95 ms per
@@ -62,7 +66,14 @@ class LruMoELayer:
         max_inserts: cap on cache inserts per step (default VLLM_R4D_LRU_MAX_INSERTS, 64); 0 is
         the static hot/cold arm -- the warm-start set stays resident and every other routed
         expert is read from the full tensor (r4d_mxfp4_moe.py.static.diff, and the README's
-        MAX_INSERTS=0 ablation)."""
+        MAX_INSERTS=0 ablation).
+
+        prefill_rows: from this many routed rows (max_tokens x top_k) on, both GEMMs run the
+        tiled prefill kernel (ops.moe_gemm_tiled: whole expert tiles, the weights streamed
+        once per tile) over the hot and the cold align, in place of the decode kernel; npw /
+        sk / wv do not apply to it. Its output equals the decode kernel's with sk = 1 bit
+        for bit. The reference runs prefill chunks through the same split path
+        (r4d_mxfp4_moe.py.lru.diff:659-696; tests/lru/test_numerics_prod.py:44-48)."""
         dev = torch.device(device)
         self.full = full
         self.full_ptrs = full.ptrs()
@@ -103,6 +114,12 @@ class LruMoELayer:
         self.s2 = torch.empty((self.mtk, self.I // 128), dtype=torch.float32, device=dev)
         self.ic3 = torch.empty((self.mtk, self.H), dtype=torch.bfloat16, device=dev)
         self.tw = torch.empty((self.mtk,), dtype=torch.float32, device=dev)
+        self.prefill = self.mtk >= prefill_rows
+        if self.prefill:
+            # the tile list of whichever align the next tiled call reads (calls are in
+            # stream order, so one list serves all of them)
+            self.tiles = torch.empty(2 * self.align[1].numel() + 1, dtype=torch.int32,
+                                     device=dev)
 
     @classmethod
     def from_profile(cls, full: ExpertWeights, profile, layer: int, budget_gb: float,
@@ -164,11 +181,17 @@ class LruMoELayer:
                         src_ptrs=[p for _, _, p in pairs])
 
     # -- _gemm_split: resident slots + the full tensor, one launch ----------------------------
-    def _gemm_split(self, y, qx, xs, slot_w, slot_s, full_w_ptr, full_s_ptr, tw, top_k, npw,
-                    sk, eh=None):
-        """eh replaces the hot align's block expert ids (the overlap's resident bucket)."""
+    def _gemm_split(self, y, qx, xs, slot_w, slot_s, part, tw, top_k, npw, sk, eh=None):
+        """part: 0 gate_up, 2 down (the index of its weight buffer in ExpertWeights.tensors);
+        eh replaces the hot align's block expert ids (the overlap's resident bucket)."""
         sh, eh0, nh, sc, ec, nc = self.align
         eh = eh0 if eh is None else eh
+        if self.prefill:
+            full = self.full.tensors()
+            self._gemm_tiled(y, qx, xs, slot_w, slot_s, sh, eh, nh, tw, top_k)
+            self._gemm_tiled(y, qx, xs, full[part], full[part + 1], sc, ec, nc, tw, top_k)
+            return
+        full_w_ptr, full_s_ptr = self.full_ptrs[part], self.full_ptrs[part + 1]
         K = qx.shape[1]
         N = slot_w.shape[1]
         rc = lib().rlu_moe_gemm_split(
@@ -182,8 +205,16 @@ class LruMoELayer:
     # -- the hot GEMM alone over a bucket of slots (the overlap's installed bucket) -----------
     def _gemm_hot(self, y, qx, xs, slot_w, slot_s, tw, top_k, npw, sk, eh):
         sh, _, nh = self.align[:3]
+        if self.prefill:
+            self._gemm_tiled(y, qx, xs, slot_w, slot_s, sh, eh, nh, tw, top_k)
+            return
         ops._r4d_fp8_moe_gemm_into(y, qx, xs, slot_w, slot_s, None, sh, eh, nh, tw, y.shape[0],
                                    top_k, self.wv, sk, npw)
+
+    # -- the tiled (prefill) GEMM over one align ----------------------------------------------
+    def _gemm_tiled(self, y, qx, xs, w, s, sorted_ids, eids, npad, tw, top_k):
+        ops.moe_gemm_tiled(y, qx, xs, w, s, sorted_ids, eids, npad, tw, y.shape[0], top_k,
+                           tiles=self.tiles)
 
     # -- _act_quant: fused silu-and-mul + group-128 quant --------------------------------------
     def _act_quant(self):
@@ -220,10 +251,10 @@ class LruMoELayer:
         if overlap:
             split_fresh(self.align[1], self.cache.miss, self.cache.n_miss, self.cache.S,
                         self.eids_res, self.eids_new)
-            self._gemm_split(*up, self.full_ptrs[0], self.full_ptrs[1], None, self.top_k,
+            self._gemm_split(*up, 0, None, self.top_k,
                              self.npw1, self.sk1, eh=self.eids_res)
             self._act_quant()
-            self._gemm_split(*down, self.full_ptrs[2], self.full_ptrs[3], tw, 1, self.npw2,
+            self._gemm_split(*down, 2, tw, 1, self.npw2,
                              self.sk2, eh=self.eids_res)
             torch.cuda.current_stream().wait_event(self.ev_up)
             self._gemm_hot(*up, None, self.top_k, self.npw1, self.sk1, self.eids_new)
@@ -233,9 +264,9 @@ class LruMoELayer:
         else:
             if waited is not None:
                 torch.cuda.current_stream().wait_stream(waited)
-            self._gemm_split(*up, self.full_ptrs[0], self.full_ptrs[1], None, self.top_k,
+            self._gemm_split(*up, 0, None, self.top_k,
                              self.npw1, self.sk1)
             self._act_quant()
-            self._gemm_split(*down, self.full_ptrs[2], self.full_ptrs[3], tw, 1, self.npw2,
+            self._gemm_split(*down, 2, tw, 1, self.npw2,
                              self.sk2)
         ops.moe_sum(self.ic3.view(M, self.top_k, self.H), output)

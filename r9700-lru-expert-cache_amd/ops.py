@@ -234,7 +234,8 @@ def moe_gemm_tiled(y: torch.Tensor, qx: torch.Tensor, x_scale: torch.Tensor, wq:
     """_r4d_fp8_moe_gemm_into for prefill-sized inputs: same operands and row contract, one
     workgroup per 128-row x 256-column tile of one expert (bit-identical to the decode kernel
     with sk = 1); N % 256 == 0. `tiles` is an int32 workspace of 2 * expert_ids.numel() + 1
-    entries."""
+    entries. wq / ws_t may be pinned host tensors (read over the bus, as the cold call's full
+    tensor is)."""
     K = qx.shape[1]
     N = wq.shape[1]
     nb = expert_ids.numel()
@@ -242,7 +243,8 @@ def moe_gemm_tiled(y: torch.Tensor, qx: torch.Tensor, x_scale: torch.Tensor, wq:
     assert qx.dtype == FP8 and wq.dtype == FP8 and wq.shape[2] == K
     tiles = moe_gemm_tiles(expert_ids, num_post_pad, tiles)
     rc = lib().rlu_moe_gemm_fp8blk_tiled(
-        _p(qx), _p(x_scale), _p(wq), _p(ws_t), _p(sorted_ids), _p(expert_ids), _p(tiles),
+        _p(qx), _p(x_scale), _P(device_ptr(wq)), _P(device_ptr(ws_t)), _p(sorted_ids),
+        _p(expert_ids), _p(tiles),
         _P(tiles.data_ptr() + 8 * nb), nb, _p(topk_weights), _p(y), mtk, top_k, K, N, wv,
         _P(stream_ptr()))
     check(rc, "rlu_moe_gemm_fp8blk_tiled")

@@ -298,3 +298,54 @@ def test_layer_overlap_read_through_and_cold_rows(pkg, pool):
         assert err <= TOL, f"step {t}: rel err {err:.3e}"
     assert any(n > 0 and c == 0 for n, c in kinds), kinds      # insert steps
     assert any(n == 0 and c > 0 for n, c in kinds), kinds      # read-through, cold rows
+
+
+def test_layer_prefill_read_through(pkg, pool):
+    """A 2048-token chunk (20480 routed rows) through apply(): the layer runs the tiled prefill
+    GEMM over the hot and the cold align (tests/lru/test_numerics_prod.py:44-48 runs the same
+    read-through chunk through the split path). Step 1 routes uniformly over all 128 experts,
+    past the read-through gate (50 distinct): no install, every non-resident expert is read
+    from pinned host memory. Step 2 routes over 30 experts, 10 of them not resident: they are
+    installed by the side-stream gather while the overlap runs. Per step: the state equals
+    the oracle's bit for bit; the output equals a decode-kernel layer's (sk = 1, no overlap)
+    bit for bit over all 2048 tokens; sampled tokens are within 2e-2 of the oracle pipeline."""
+    M = 2048
+    _, perm0 = trace.zipf_trace(seed=600, E=E, rows=20, k=TOPK, steps=1, s=1.1)
+    hot, rank = trace.warm_hot(perm0, S)
+    full = pkg.ExpertWeights(pool["w13"], pool["w13s"], pool["w2"], pool["w2s"])
+    a = pkg.LruMoELayer(full, hot, rank, M, TOPK, DEV)
+    b = pkg.LruMoELayer(full, hot, rank, M, TOPK, DEV, sk1=1, sk2=1, prefill_rows=1 << 30)
+    assert a.prefill and not b.prefill
+    st = olru.warm_start(E, S, hot, rank)
+    rng = np.random.default_rng(600)
+    cold = [e for e in range(E) if e not in set(hot)]
+    narrow = np.array(sorted(list(hot[:20]) + cold[:10]), dtype=np.int32)
+    side = torch.cuda.Stream()
+    for t, pool_ids in enumerate((np.arange(E, dtype=np.int32), narrow)):
+        ids = np.stack([rng.choice(pool_ids, TOPK, replace=False) for _ in range(M)]).astype(np.int32)
+        x = fp8.bf16_round(rng.standard_normal((M, H)).astype(np.float32))
+        tw = rng.random((M, TOPK)).astype(np.float32)
+        xd = torch.from_numpy(x).to(torch.bfloat16).to(DEV)
+        twd, idd = torch.from_numpy(tw).to(DEV), torch.from_numpy(ids).to(DEV)
+        oa = torch.full((M, H), float("nan"), dtype=torch.bfloat16, device=DEV)
+        ob = torch.full_like(oa, float("nan"))
+        gpu_case(f"prefill layer step {t}: tiled")
+        a.apply(oa, xd, twd, idd, gather=True, side=side)
+        gpu_case(f"prefill layer step {t}: decode kernel")
+        b.apply(ob, xd, twd, idd, gather=True, side=side)
+        torch.cuda.synchronize()
+        olru.fused(st, ids.reshape(-1), 16)
+        for name, ga in zip(olru.LruState.NAMES, a.cache.state()):
+            if name == "routed":
+                continue
+            assert np.array_equal(ga.cpu().numpy(), getattr(st, name)), (t, name)
+        if t == 0:
+            assert int(st.n_miss[0]) == 0 and (st.map_cold[ids.reshape(-1)] >= 0).any()
+        else:
+            assert int(st.n_miss[0]) == 10
+        assert not torch.isnan(oa).any()
+        assert torch.equal(oa.view(torch.int16), ob.view(torch.int16)), f"step {t}"
+        pick = np.sort(rng.choice(M, 96, replace=False))
+        ref = oracle_layer(x[pick], ids[pick], tw[pick], pool)
+        err = ogemm.rel_err(oa.float().cpu().numpy()[pick], ref)
+        assert err <= TOL, f"step {t}: rel err {err:.3e}"
