@@ -185,6 +185,20 @@ int rlu_moe_gemm_fp8blk_tiled(const void* qx, const float* xs, const void* wq, c
                               void* y, int mtk, int top_k, int K, int N, int wv,
                               hipStream_t stream);
 
+/* No counterpart in the reference (which runs rlu_moe_gemm_fp8blk_tiled's output through the
+ * separate SiLU-mul-quant, r4d_mxfp4_moe.py.lru.diff:640-657): gate_up with SiLU-mul-quant in
+ * the epilogue. q2 [mtk, N/2] e4m3 and s2 [mtk, N/256] float (group-128 scales) equal
+ * rlu_silu_mul_quant(group 128) of rlu_moe_gemm_fp8blk_tiled's bf16 output bit for bit, rows
+ * the align does not name untouched; the [mtk, N] bf16 intermediate is never written. Built
+ * for K = 2560 and N % 256 == 0: other shapes return -6 before any other check, so a call with
+ * mtk = 0 is a capability query (0: built; nothing is launched). Otherwise -1 / -2 as
+ * rlu_moe_gemm_fp8blk_tiled. */
+int rlu_moe_gemm_fp8blk_tiled_silu_quant(const void* qx, const float* xs, const void* wq,
+                                         const float* ws, const int* sorted_ids,
+                                         const int* expert_ids, const int* tiles,
+                                         const int* ntiles, int max_tiles, void* q2, float* s2,
+                                         int mtk, int top_k, int K, int N, hipStream_t stream);
+
 /* No counterpart in the reference. For callers that cannot allocate -- code recorded into a HIP
  * graph, serving loops and harnesses that forbid hipMalloc: rlu_moe_gemm_tiles followed by
  * rlu_moe_gemm_fp8blk_tiled (same kernels, same results bit for bit) with the tile list kept in

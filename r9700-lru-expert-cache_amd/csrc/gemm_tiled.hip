@@ -354,4 +354,27 @@ int rlu_moe_gemm_fp8blk_tiled_noalloc(const void* qx, const float* xs, const voi
   return (int)hipGetLastError();
 }
 
+// The gate_up GEMM with SiLU-mul-quant fused into its epilogue (prefill.hip, ACT): q2 / s2
+// equal rlu_silu_mul_quant (group 128) of rlu_moe_gemm_fp8blk_tiled's bf16 output bit for bit,
+// without that [mtk, N] output. Built for K = 2560 (gate_up of the 2560-wide model) and N % 256
+// == 0; other shapes return -6 before anything else is checked, so a call with mtk = 0 is a
+// capability query (0: built, nothing launched).
+int rlu_moe_gemm_fp8blk_tiled_silu_quant(const void* qx, const float* xs, const void* wq,
+                                         const float* ws, const int* sorted_ids,
+                                         const int* expert_ids, const int* tiles,
+                                         const int* ntiles, int max_tiles, void* q2, float* s2,
+                                         int mtk, int top_k, int K, int N,
+                                         hipStream_t stream) {
+  using namespace rlu::tiled;
+  if (!rlu::prefill_stream_act_built(K, N)) return -6;
+  const int rc = check_gemm_args(mtk, top_k, K, N, max_tiles, 0);
+  if (rc) return rc;
+  if (mtk == 0) return 0;
+  if (!q2 || !s2) return -1;
+  if (rlu::launch_prefill_stream_act(qx, xs, wq, ws, sorted_ids, expert_ids, tiles, ntiles,
+                                     max_tiles, q2, s2, mtk, top_k, K, N, stream))
+    return -6;
+  return (int)hipGetLastError();
+}
+
 }  // extern "C"

@@ -39,6 +39,7 @@
 #include "gemm_common.h"
 #include "numerics.h"
 #include "prefill.h"
+#include "quant_row.h"
 #include "wave.h"
 
 namespace rlu {
@@ -60,6 +61,8 @@ struct Args {
   const int* ntiles;
   uint16_t* y;
   const float* tw;
+  uint8_t* q2;
+  float* s2;
   int mtk;
   int top_k;
   int N;
@@ -97,14 +100,22 @@ struct Cfg {
   static_assert(BP >= 1, "an epilogue pass holds at least one block");
 };
 
-template <int NK, int W, int S, int KC, int D, int BR, int BG, bool TWT>
+// ACT: the gate_up GEMM with SiLU-mul-quant in its epilogue. N = 2 I (gate | up); item g
+// covers gate columns [128 g, 128 g + 128) (waves 0 .. W/2 - 1) and the matching up columns
+// [I + 128 g, ...) (the other waves), so each output row's 128-column activation group is
+// whole in one item. The epilogue writes q2 [mtk, I] e4m3 and s2 [mtk, I / 128] instead of y,
+// computed from the bf16-rounded GEMM outputs exactly as silu_mul_quant_k computes them from
+// y (same silu, product and amax reduction, same rounding).
+template <int NK, int W, int S, int KC, int D, int BR, int BG, bool TWT, bool ACT>
 __global__ __launch_bounds__(W * WAVE) void stream_k(
     const uint8_t* __restrict__ qx, const float* __restrict__ xs, const uint8_t* __restrict__ wq,
     const float* __restrict__ ws, const int* __restrict__ sorted_ids,
     const int* __restrict__ eids, const int* __restrict__ tiles, const int* __restrict__ ntiles,
-    uint16_t* __restrict__ y, const float* __restrict__ tw, int mtk, int top_k, int N) {
+    uint16_t* __restrict__ y, const float* __restrict__ tw, uint8_t* __restrict__ q2,
+    float* __restrict__ s2, int mtk, int top_k, int N) {
   using CF = Cfg<NK, W, S, KC, D, BR, BG>;
   constexpr int K = CF::K, NCH = CF::NCH, C = CF::C, BPW = CF::BPW, XQ = CF::XQ;
+  static_assert(!ACT || (C == 256 && !TWT), "an activation item is 128 gate + 128 up columns");
   extern __shared__ __align__(16) unsigned char smem[];
   float* sx = reinterpret_cast<float*>(smem);
   int* rows = reinterpret_cast<int*>(sx + CF::SX);
@@ -125,6 +136,12 @@ __global__ __launch_bounds__(W * WAVE) void stream_k(
     return *reinterpret_cast<const v4u*>(smem + abase[q] + off);
   };
   const int ncg = N / C;
+  // first output column of this wave's strips in an item starting at column n0
+  auto col0 = [&](int n0) __attribute__((always_inline)) -> int {
+    if (!ACT) return n0 + w * S * 16;
+    const int j = w * S * 16;
+    return j < 128 ? n0 / 2 + j : N / 2 + n0 / 2 + j - 128;
+  };
   const int nx = gridDim.x % NXCD == 0 ? NXCD : 1;
   const int xcd = (int)blockIdx.x % nx, per = (int)gridDim.x / nx;
   const int nt = ntiles[0];
@@ -147,7 +164,7 @@ __global__ __launch_bounds__(W * WAVE) void stream_k(
   // h 1024 + lane 16 (the base and the step offset stay in scalar registers)
   auto wbase = [&](const Item& it) __attribute__((always_inline)) {
     return __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(wq + ((size_t)it.e * N + it.n0 + w * S * 16) * K), 0, S * 16 * K, BUF_WORD3);
+        (void*)(wq + ((size_t)it.e * N + col0(it.n0)) * K), 0, S * 16 * K, BUF_WORD3);
   };
   // the sorted id of row r16 of block blk of an item (mtk past the tile): one vector load,
   // issued at an item's start and used at its last chunk, so waiting for it costs nothing
@@ -271,7 +288,7 @@ __global__ __launch_bounds__(W * WAVE) void stream_k(
         for (int s = 0; s < S; ++s) acc[bk][s] = v4f{0.f, 0.f, 0.f, 0.f};
       // the weight-block scales of this wave's strips, one per step: scalar loads (they never
       // enter the vector-memory counter the weight ring waits on)
-      const float* wsrow = ws + ((size_t)mA.e * (N / 128) + (mA.n0 + w * S * 16) / 128) * NK;
+      const float* wsrow = ws + ((size_t)mA.e * (N / 128) + col0(mA.n0) / 128) * NK;
       float wsr[NK];
 #pragma unroll
       for (int k = 0; k < NK; ++k) wsr[k] = wsrow[k];
@@ -356,6 +373,35 @@ __global__ __launch_bounds__(W * WAVE) void stream_k(
             }
             __syncthreads();
             const int nr = ((mA.nbk < p0 + CF::BP ? mA.nbk : p0 + CF::BP) - p0) * 16;
+            if (ACT) {
+              // one 16-lane row group per output row, lane l on columns [8 l, 8 l + 8) of the
+              // item's 128-column group (nr is a multiple of 16, so every wave's four groups
+              // run the same trip count and the DPP reduction sees whole groups)
+              const int I = N / 2, g = mA.n0 / C, l16 = lane & 15;
+              for (int rr = (int)threadIdx.x / 16; rr < nr; rr += W * 4) {
+                float gv[8], uv[8], a[8];
+                unpack8_bf16(*reinterpret_cast<const uint4*>(ot + rr * C + 8 * l16), gv);
+                unpack8_bf16(*reinterpret_cast<const uint4*>(ot + rr * C + 128 + 8 * l16), uv);
+                uint32_t mx = 0;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                  a[j] = bf16_to_f32(f32_to_bf16(__fmul_rn(silu_bf16(gv[j]), uv[j])));
+                  mx = max(mx, abs_bits(a[j]));
+                }
+                const float sc = scale_of(row_max_u32(mx));
+                const uint2 qv = quant8(a, sc);
+                const int so = rows[par * TB * 16 + p0 * 16 + rr];
+                if (so < mtk) {
+                  typedef unsigned v2u __attribute__((ext_vector_type(2)));
+                  __builtin_nontemporal_store(
+                      v2u{qv.x, qv.y},
+                      reinterpret_cast<v2u*>(q2 + (size_t)so * I + g * 128 + 8 * l16));
+                  if (l16 == 0) __builtin_nontemporal_store(sc, s2 + (size_t)so * (I / 128) + g);
+                }
+              }
+              __syncthreads();
+              continue;
+            }
             constexpr int CH = C / 8;                     // 16-byte chunks per row
             for (int u = (int)threadIdx.x; u < nr * CH; u += W * WAVE) {
               const int rr = u / CH, ch = u - rr * CH;
@@ -386,22 +432,28 @@ __global__ __launch_bounds__(W * WAVE) void stream_k(
   }
 }
 
-template <int NK, int W, int S, int KC, int D, int BR = 1, int BG = 2, int OCC = 1>
+// ACT_CFG: the configuration of the SiLU-mul-quant variant (built only for it), else of the
+// plain kernels
+template <int NK, int W, int S, int KC, int D, bool ACT_CFG = false, int BR = 1, int BG = 2,
+          int OCC = 1>
 static int launch_cfg(const Args& a, int max_tiles, hipStream_t stream) {
   using CF = Cfg<NK, W, S, KC, D, BR, BG>;
   if (a.N % CF::C) return -1;
+  if ((a.q2 != nullptr) != ACT_CFG || (a.q2 && (a.tw || CF::C != 256))) return -1;
   const int items = max_tiles * (a.N / CF::C);
   int grid = device_cus() * OCC;
   if (grid > items) grid = items;
   if (grid >= NXCD) grid -= grid % NXCD;
-#define RLU_PF(T)                                                                             \
-  hipLaunchKernelGGL((stream_k<NK, W, S, KC, D, BR, BG, T>), dim3(grid), dim3(W * WAVE), CF::LDS, stream, \
-                     a.qx, a.xs, a.wq, a.ws, a.sorted_ids, a.eids, a.tiles, a.ntiles, a.y, a.tw, \
-                     a.mtk, a.top_k, a.N)
-  if (a.tw)
-    RLU_PF(true);
+#define RLU_PF(T, A)                                                                          \
+  hipLaunchKernelGGL((stream_k<NK, W, S, KC, D, BR, BG, T, A>), dim3(grid), dim3(W * WAVE),     \
+                     CF::LDS, stream, a.qx, a.xs, a.wq, a.ws, a.sorted_ids, a.eids, a.tiles,    \
+                     a.ntiles, a.y, a.tw, a.q2, a.s2, a.mtk, a.top_k, a.N)
+  if constexpr (ACT_CFG)
+    RLU_PF(false, true);
+  else if (a.tw)
+    RLU_PF(true, false);
   else
-    RLU_PF(false);
+    RLU_PF(false, false);
 #undef RLU_PF
   return 0;
 }
@@ -412,11 +464,24 @@ int launch_prefill_stream(const void* qx, const float* xs, const void* wq, const
                           const int* sorted_ids, const int* expert_ids, const int* tiles,
                           const int* ntiles, int max_tiles, const float* topk_weights, void* y,
                           int mtk, int top_k, int K, int N, hipStream_t stream) {
-  const pf::Args a{(const uint8_t*)qx, xs,         (const uint8_t*)wq, ws,    sorted_ids,
-                   expert_ids,         tiles,      ntiles,             (uint16_t*)y,
-                   topk_weights,       mtk,        top_k,              N};
+  const pf::Args a{(const uint8_t*)qx, xs,      (const uint8_t*)wq, ws,  sorted_ids,
+                   expert_ids,         tiles,   ntiles,             (uint16_t*)y,
+                   topk_weights,       nullptr, nullptr,            mtk, top_k, N};
   if (K == 2560) return pf::launch_cfg<20, 8, 2, 4, 5>(a, max_tiles, stream);
   if (K == 768) return pf::launch_cfg<6, 8, 2, 3, 6>(a, max_tiles, stream);
+  return -1;
+}
+
+bool prefill_stream_act_built(int K, int N) { return K == 2560 && N % 256 == 0; }
+
+int launch_prefill_stream_act(const void* qx, const float* xs, const void* wq, const float* ws,
+                              const int* sorted_ids, const int* expert_ids, const int* tiles,
+                              const int* ntiles, int max_tiles, void* q2, float* s2, int mtk,
+                              int top_k, int K, int N, hipStream_t stream) {
+  const pf::Args a{(const uint8_t*)qx, xs,          (const uint8_t*)wq, ws,  sorted_ids,
+                   expert_ids,         tiles,       ntiles,             nullptr,
+                   nullptr,            (uint8_t*)q2, s2,                mtk, top_k, N};
+  if (K == 2560) return pf::launch_cfg<20, 8, 2, 4, 4, true>(a, max_tiles, stream);
   return -1;
 }
 

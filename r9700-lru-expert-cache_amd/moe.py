@@ -109,12 +109,16 @@ class LruMoELayer:
         self.route_capture = None
         self.qx = torch.empty((self.M, self.H), dtype=ops.FP8, device=dev)
         self.xs = torch.empty((self.M, self.H // 128), dtype=torch.float32, device=dev)
-        self.ic1 = torch.empty((self.mtk, self.N1), dtype=torch.bfloat16, device=dev)
+        self.prefill = self.mtk >= prefill_rows
+        # prefill gate_up with SiLU-mul-quant in its epilogue where a kernel is built for the
+        # shape: no [mtk, 2I] bf16 intermediate (same q2 / s2 bits)
+        self.fuse_act = self.prefill and ops.moe_gemm_tiled_silu_quant_built(self.H, self.N1)
+        self.ic1 = (None if self.fuse_act else
+                    torch.empty((self.mtk, self.N1), dtype=torch.bfloat16, device=dev))
         self.q2 = torch.empty((self.mtk, self.I), dtype=ops.FP8, device=dev)
         self.s2 = torch.empty((self.mtk, self.I // 128), dtype=torch.float32, device=dev)
         self.ic3 = torch.empty((self.mtk, self.H), dtype=torch.bfloat16, device=dev)
         self.tw = torch.empty((self.mtk,), dtype=torch.float32, device=dev)
-        self.prefill = self.mtk >= prefill_rows
         if self.prefill:
             # the tile list of whichever align the next tiled call reads (calls are in
             # stream order, so one list serves all of them)
@@ -220,6 +224,24 @@ class LruMoELayer:
     def _act_quant(self):
         ops.silu_mul_quant(self.ic1, group=ops.GROUP, out=(self.q2, self.s2))
 
+    # -- gate_up and the activation quant over the hot align (block ids eh) and, with cold,
+    # the cold align -------------------------------------------------------------------------
+    def _gate_up_act(self, eh=None, cold=True):
+        if self.fuse_act:
+            sh, eh0, nh, sc, ec, nc = self.align
+            for w, s, al in (((self.slots.w13, self.slots.s13, (sh, eh0 if eh is None else eh,
+                                                               nh)),) +
+                             (((self.full.w13, self.full.s13, (sc, ec, nc)),) if cold else ())):
+                ops.moe_gemm_tiled_silu_quant(self.q2, self.s2, self.qx, self.xs, w, s, *al,
+                                              self.mtk, self.top_k, tiles=self.tiles)
+            return
+        up = (self.ic1, self.qx, self.xs, self.slots.w13, self.slots.s13)
+        if cold:
+            self._gemm_split(*up, 0, None, self.top_k, self.npw1, self.sk1, eh=eh)
+        else:
+            self._gemm_hot(*up, None, self.top_k, self.npw1, self.sk1, eh)
+        self._act_quant()
+
     def apply(self, output: torch.Tensor, hidden_states: torch.Tensor, topk_weights: torch.Tensor,
               topk_ids: torch.Tensor, gather: bool = True,
               side: torch.cuda.Stream | None = None, overlap: bool | None = None) -> None:
@@ -246,27 +268,19 @@ class LruMoELayer:
         if tw.dtype != torch.float32 or not tw.is_contiguous():   # as fused_topk already gives
             self.tw.copy_(tw)
             tw = self.tw
-        up = (self.ic1, self.qx, self.xs, self.slots.w13, self.slots.s13)
         down = (self.ic3, self.q2, self.s2, self.slots.w2, self.slots.s2)
         if overlap:
             split_fresh(self.align[1], self.cache.miss, self.cache.n_miss, self.cache.S,
                         self.eids_res, self.eids_new)
-            self._gemm_split(*up, 0, None, self.top_k,
-                             self.npw1, self.sk1, eh=self.eids_res)
-            self._act_quant()
-            self._gemm_split(*down, 2, tw, 1, self.npw2,
-                             self.sk2, eh=self.eids_res)
+            self._gate_up_act(eh=self.eids_res)
+            self._gemm_split(*down, 2, tw, 1, self.npw2, self.sk2, eh=self.eids_res)
             torch.cuda.current_stream().wait_event(self.ev_up)
-            self._gemm_hot(*up, None, self.top_k, self.npw1, self.sk1, self.eids_new)
-            self._act_quant()
+            self._gate_up_act(eh=self.eids_new, cold=False)
             torch.cuda.current_stream().wait_stream(waited)
             self._gemm_hot(*down, tw, 1, self.npw2, self.sk2, self.eids_new)
         else:
             if waited is not None:
                 torch.cuda.current_stream().wait_stream(waited)
-            self._gemm_split(*up, 0, None, self.top_k,
-                             self.npw1, self.sk1)
-            self._act_quant()
-            self._gemm_split(*down, 2, tw, 1, self.npw2,
-                             self.sk2)
+            self._gate_up_act()
+            self._gemm_split(*down, 2, tw, 1, self.npw2, self.sk2)
         ops.moe_sum(self.ic3.view(M, self.top_k, self.H), output)

@@ -250,6 +250,37 @@ def moe_gemm_tiled(y: torch.Tensor, qx: torch.Tensor, x_scale: torch.Tensor, wq:
     check(rc, "rlu_moe_gemm_fp8blk_tiled")
 
 
+def moe_gemm_tiled_silu_quant_built(K: int, N: int) -> bool:
+    """Whether moe_gemm_tiled_silu_quant has a kernel for gate_up weights [*, N, K] (a
+    zero-row call: nothing is launched)."""
+    rc = lib().rlu_moe_gemm_fp8blk_tiled_silu_quant(
+        *([_P(0)] * 8), 1, _P(0), _P(0), 0, 1, K, N, _P(0))
+    return rc == 0
+
+
+def moe_gemm_tiled_silu_quant(q2: torch.Tensor, s2: torch.Tensor, qx: torch.Tensor,
+                              x_scale: torch.Tensor, wq: torch.Tensor, ws_t: torch.Tensor,
+                              sorted_ids: torch.Tensor, expert_ids: torch.Tensor,
+                              num_post_pad: torch.Tensor, mtk: int, top_k: int,
+                              tiles: torch.Tensor | None = None) -> None:
+    """moe_gemm_tiled of gate_up followed by silu_mul_quant (group 128) in one kernel: q2
+    [mtk, N/2] e4m3 and s2 [mtk, N/256] f32 equal silu_mul_quant(moe_gemm_tiled(...)) bit for
+    bit, rows the align does not name untouched. Raises for shapes without a kernel
+    (moe_gemm_tiled_silu_quant_built)."""
+    K = qx.shape[1]
+    N = wq.shape[1]
+    nb = expert_ids.numel()
+    assert q2.shape == (mtk, N // 2) and q2.dtype == FP8 and q2.is_contiguous()
+    assert s2.shape == (mtk, N // 256) and s2.dtype == torch.float32 and s2.is_contiguous()
+    assert qx.dtype == FP8 and wq.dtype == FP8 and wq.shape[2] == K
+    tiles = moe_gemm_tiles(expert_ids, num_post_pad, tiles)
+    rc = lib().rlu_moe_gemm_fp8blk_tiled_silu_quant(
+        _p(qx), _p(x_scale), _P(device_ptr(wq)), _P(device_ptr(ws_t)), _p(sorted_ids),
+        _p(expert_ids), _p(tiles), _P(tiles.data_ptr() + 8 * nb), nb, _p(q2), _p(s2), mtk,
+        top_k, K, N, _P(stream_ptr()))
+    check(rc, "rlu_moe_gemm_fp8blk_tiled_silu_quant")
+
+
 NOALLOC_MAX_BLOCKS = 8192      # the scratch tile list's capacity (131072 sorted ids)
 
 

@@ -276,3 +276,24 @@ def test_prefill_4096x512_tiled_vs_decode_and_oracle(pkg, pool, prefill, which):
     got = yt.float().cpu().numpy()
     err = ogemm.rel_err(got[rows], ref[rows])
     assert err <= 1e-2, f"{which}: rel err {err:.3e}"
+
+
+def test_prefill_4096x512_gate_up_silu_quant_fused(pkg, pool, prefill):
+    """gate_up with SiLU-mul-quant in its epilogue equals silu_mul_quant of the tiled gate_up
+    output bit for bit over all 40960 rows (q2 and the group-128 scales)."""
+    ops = pkg.ops
+    sh, eh, nh = prefill["al"][:3]
+    mtk = prefill["ids"].size
+    assert ops.moe_gemm_tiled_silu_quant_built(H, 2 * I)
+    y = torch.empty((mtk, 2 * I), dtype=torch.bfloat16, device=DEV)
+    ops.moe_gemm_tiled(y, prefill["qx"], prefill["xs"], pool["w13_dev"], pool["w13s_dev"], sh,
+                       eh, nh, None, mtk, TOPK)
+    _, q_ref, s_ref = ops.silu_mul_quant(y)
+    q = torch.full((mtk, I), 0x7F, dtype=torch.uint8, device=DEV).view(ops.FP8)
+    s = torch.full((mtk, I // 128), float("nan"), device=DEV)
+    gpu_case("C5 prefill gate_up + silu-mul-quant fused")
+    ops.moe_gemm_tiled_silu_quant(q, s, prefill["qx"], prefill["xs"], pool["w13_dev"],
+                                  pool["w13s_dev"], sh, eh, nh, mtk, TOPK)
+    torch.cuda.synchronize()
+    assert torch.equal(q.view(torch.uint8), q_ref.view(torch.uint8))
+    assert torch.equal(s.view(torch.int32), s_ref.view(torch.int32))

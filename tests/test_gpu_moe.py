@@ -545,6 +545,51 @@ def test_moe_gemm_tiled_equals_decode_kernel(ops, layer, M, wv):
         assert ogemm.rel_err(np_from_bf16(yt), want) <= TOL
 
 
+@pytest.mark.parametrize("M", [256, 600])
+def test_moe_gemm_tiled_silu_quant_fused(ops, layer, M):
+    """gate_up with SiLU-mul-quant in the streamed kernel's epilogue: q2 / s2 equal
+    silu_mul_quant of the tiled gate_up output bit for bit on every row the align names; rows
+    it does not name (a block set to expert -1) keep their contents. Built for K = 2560 only:
+    the down shape (K = 768) reports no kernel and the call raises."""
+    E, H, I = layer["E"], layer["H"], layer["I"]
+    top_k = 10
+    assert ops.moe_gemm_tiled_silu_quant_built(H, 2 * I)
+    assert not ops.moe_gemm_tiled_silu_quant_built(I, H)
+    ids = routing(M, top_k, E, seed=M + 7)
+    mtk = ids.size
+    s, e, n = align_all(ids, E)
+    e2 = e.copy()
+    e2[1] = -1
+    al = to_dev_i32(s, e2, n)
+    x = fp8.bf16_round(np.random.default_rng(M + 7).standard_normal((M, H)).astype(np.float32))
+    qx, xs = fp8.group_quant(x, 128)
+    qx_t = torch.from_numpy(qx).to(DEV).view(torch.float8_e4m3fn)
+    xs_t = torch.from_numpy(xs).to(DEV)
+    y = torch.zeros((mtk, 2 * I), dtype=torch.bfloat16, device=DEV)
+    ops.moe_gemm_tiled(y, qx_t, xs_t, layer["w13t"], layer["w13s"], *al, None, mtk, top_k)
+    _, q_ref, s_ref = ops.silu_mul_quant(y)
+    q = torch.full((mtk, I), 0x7F, dtype=torch.uint8, device=DEV).view(ops.FP8)
+    sc = torch.full((mtk, I // 128), float("nan"), device=DEV)
+    gpu_case(f"tiled gate_up + silu-mul-quant M={M}")
+    ops.moe_gemm_tiled_silu_quant(q, sc, qx_t, xs_t, layer["w13t"], layer["w13s"], *al, mtk,
+                                  top_k)
+    torch.cuda.synchronize()
+    live = np.zeros(mtk, bool)
+    live[s[:n[0]][s[:n[0]] < mtk]] = True
+    live[s[16:32][s[16:32] < mtk]] = False
+    lv = torch.from_numpy(live).to(DEV)
+    qb = q.view(torch.uint8)
+    assert torch.equal(qb[lv], q_ref.view(torch.uint8)[lv])
+    assert torch.equal(sc[lv].view(torch.int32), s_ref[lv].view(torch.int32))
+    assert bool((qb[~lv] == 0x7F).all()) and bool(torch.isnan(sc[~lv]).all())
+    a2 = torch.zeros((mtk, I), dtype=ops.FP8, device=DEV)          # down-shaped operands
+    with pytest.raises(RuntimeError, match="rc=-6"):
+        ops.moe_gemm_tiled_silu_quant(
+            torch.empty((mtk, H // 2), dtype=ops.FP8, device=DEV),
+            torch.empty((mtk, H // 256), device=DEV), a2, torch.ones((mtk, I // 128), device=DEV),
+            layer["w2t"], layer["w2s"], *al, mtk, 1)
+
+
 def test_moe_gemm_tiled_row_contract_and_graph(ops, layer):
     """A block of expert -1 is skipped (its rows stay NaN); graph replay equals eager."""
     E, H, I = layer["E"], layer["H"], layer["I"]
