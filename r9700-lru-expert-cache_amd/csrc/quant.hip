@@ -16,6 +16,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "gemm_common.h"
 #include "numerics.h"
 #include "quant_row.h"
 #include "rlu.h"
@@ -129,6 +130,50 @@ __global__ __launch_bounds__(QT) void silu_mul_quant_k(const uint16_t* __restric
   }
 }
 
+// The group-128 form of silu_mul_quant_k laid out by (row, 128-column group) units rather than
+// by rows: a 16-lane group takes one unit (lane l on columns [8 l, 8 l + 8), so the DPP row is the
+// quant group), a workgroup 16 units, and the grid strides over all rows x d / 128 units. Same
+// arithmetic as silu_mul_quant_k, bit for bit; a row-per-workgroup launch leaves most of its
+// threads idle at d = 768 and spends its time dispatching workgroups once rows run to
+// thousands (a prefill chunk's 40960).
+constexpr int SQ_UNITS = 16;                         // units per 256-thread workgroup
+
+__global__ __launch_bounds__(QT) void silu_mul_quant_g128_k(const uint16_t* __restrict__ x,
+                                                            int rows, int d, int ldx,
+                                                            uint8_t* __restrict__ q,
+                                                            float* __restrict__ scale,
+                                                            uint16_t* __restrict__ act) {
+  const int ng = d / 128;
+  const long long units = (long long)rows * ng;
+  const int l16 = (int)threadIdx.x & 15;
+  // every lane of a 16-lane group has the same unit, so a group runs whole or not at all
+  for (long long u = (long long)blockIdx.x * SQ_UNITS + threadIdx.x / 16; u < units;
+       u += (long long)gridDim.x * SQ_UNITS) {
+    const int row = (int)(u / ng), grp = (int)(u - (long long)row * ng);
+    const int c = grp * 128 + 8 * l16;
+    const uint16_t* g = x + (size_t)row * ldx;
+    float gv[8], uv[8], a[8];
+    load8_bf16(g + c, gv);
+    load8_bf16(g + d + c, uv);
+    uint32_t m = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      a[j] = bf16_to_f32(f32_to_bf16(__fmul_rn(silu_bf16(gv[j]), uv[j])));
+      m = max(m, abs_bits(a[j]));
+    }
+    const float s = scale_of(row_max_u32(m));
+    *reinterpret_cast<uint2*>(q + (size_t)row * d + c) = quant8(a, s);
+    if (l16 == 0) scale[(size_t)row * ng + grp] = s;
+    if (act) {
+      uint32_t w[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        w[j] = (uint32_t)f32_to_bf16(a[2 * j]) | ((uint32_t)f32_to_bf16(a[2 * j + 1]) << 16);
+      *reinterpret_cast<uint4*>(act + (size_t)row * d + c) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+  }
+}
+
 // out [M, H] = sum over k of in [M * top_k + k, H]; grid (M, ceil(H / (QT*8)))
 // moe_sum rows loaded together: with top_k 10 all ten loads are in flight at once (the rows
 // are read in one memory round trip instead of ten, 3.82 -> 3.71 ms per 52-layer B=4 step)
@@ -189,6 +234,16 @@ int rlu_silu_mul_quant(const void* x, int rows, int d, int ldx, int group, void*
   if (!(group == 0 || (group == 128 && d % 128 == 0))) return -2;
   if (group == 0 && d > rlu::QT * 8 * 4) return -3;
   if (rows == 0) return 0;
+  if (group == 128) {
+    const long long units = (long long)rows * (d / 128);
+    long long grid = (units + rlu::SQ_UNITS - 1) / rlu::SQ_UNITS;
+    const long long cap = 16LL * rlu::device_cus();
+    if (grid > cap) grid = cap;
+    hipLaunchKernelGGL(rlu::silu_mul_quant_g128_k, dim3((unsigned)grid), dim3(rlu::QT), 0,
+                       stream, (const uint16_t*)x, rows, d, ldx, (uint8_t*)q, scale,
+                       (uint16_t*)act);
+    return (int)hipGetLastError();
+  }
   hipLaunchKernelGGL(rlu::silu_mul_quant_k, dim3(rows), dim3(rlu::QT), 0, stream,
                      (const uint16_t*)x, d, ldx, group, (uint8_t*)q, scale, (uint16_t*)act);
   return (int)hipGetLastError();

@@ -51,6 +51,8 @@ def ops(pkg):
 # ---- quantizers ------------------------------------------------------------------------------
 SILU_CASES = [(r, d, s, g) for r in (1, 10, 50, 80, 2048) for d in (320, 640, 768)
               for s in (1.0, 1e-3, 60.0) for g in (0, 128) if not (g == 128 and d % 128)]
+# past the group-128 kernel's grid cap (16 workgroups per CU x 16 units): its grid-stride loop
+SILU_CASES += [(12000, 768, 1.0, 128)]
 
 
 @pytest.mark.parametrize("rows,d,scale_in,group", SILU_CASES)
@@ -267,9 +269,10 @@ def test_moe_gemm2_routed_weight_vs_oracle(ops, layer, npw, M, sk):
     assert err <= TOL, f"rel err {err:.3e}"
 
 
-def test_moe_gemm_row_contract(ops, layer):
+@pytest.mark.parametrize("sk", [0, 1])
+def test_moe_gemm_row_contract(ops, layer, sk):
     """tests/k1/moe_ref_harness.py:282-321: only live rows written; expert -1 skips its block;
-    num_post_pad is honoured on the device."""
+    num_post_pad is honoured on the device; sk = 0 (auto split) and sk = 1."""
     E, H, I = layer["E"], layer["H"], layer["I"]
     M, top_k = 8, 10
     ids = routing(M, top_k, E, seed=11)
@@ -283,11 +286,11 @@ def test_moe_gemm_row_contract(ops, layer):
     def written(s_, e_, n_):
         y = torch.full((mtk, 2 * I), float("nan"), dtype=torch.bfloat16, device=DEV)
         run_gemm(ops, y, qx_t, xs_t, layer["w13t"], layer["w13s"], to_dev_i32(s_, e_, n_), None,
-                 mtk, top_k)
+                 mtk, top_k, sk=sk)
         torch.cuda.synchronize()
         return ~torch.isnan(y).any(dim=1).cpu().numpy(), y
 
-    gpu_case("moe gemm row contract")
+    gpu_case(f"moe gemm row contract sk={sk}")
     w0, y0 = written(s, e, n)
     live = np.zeros(mtk, bool)
     live[s[:n[0]][s[:n[0]] < mtk]] = True
