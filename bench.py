@@ -512,10 +512,18 @@ def counter_probe(torch, pkg, dev, calls=50):
         torch.cuda.synchronize()
         assert int(cache.n_miss.item()) == k
     res = prefill_gemm(torch, pkg, dev, reps=3, lru=False)
+    # the calibration kernel of known size for FETCH_SIZE / WRITE_SIZE: a 256 MiB device copy,
+    # the run's last copy dispatch
+    a = torch.ones(256 << 20, dtype=torch.uint8, device=dev)
+    c = torch.empty_like(a)
+    torch.cuda.synchronize()
+    c.copy_(a)
+    torch.cuda.synchronize()
     print(json.dumps({"counter_probe": f"lru_k: {calls} calls at 0 inserts, then {calls} at 64 "
                                        "(mk 200); then the prefill kernels (4096 tokens): "
-                                       "gate_up, down, SiLU-mul-quant, fused gate_up x4 each",
-                      "prefill": res}), flush=True)
+                                       "gate_up, down, SiLU-mul-quant, fused gate_up x4 each; "
+                                       "then one 256 MiB device-to-device copy",
+                      "copy_bytes": 256 << 20, "prefill": res}), flush=True)
 
 
 # ---- host-link traffic and the hot-profile routing ----------------------------------------------

@@ -201,18 +201,23 @@ def pack_fp8_block(w: torch.Tensor, rows: int = 4096) -> tuple[torch.Tensor, tor
     """bf16/fp32 [N, K] -> (e4m3 [N, K] in fragment order, fp32 block scales [N/128, K/128]):
     per 128x128 block scale = max(amax, 1e-12) / 448, q = e4m3(clamp(w / scale, +-448))
     (kernels/fp8_target_lmhead.py:44-66), quantized in row chunks so the fp32 temporaries stay
-    small."""
+    small. Each chunk is shuffled straight into the output (the permutation stays inside 16-row
+    strips and chunks are whole strips), so the peak is one fp8 weight plus one chunk, not two
+    full-size fp8 copies."""
     N, K = w.shape
     assert N % 128 == 0 and K % 128 == 0, (N, K)
-    q = torch.empty((N, K), dtype=FP8, device=w.device)
+    rows = max(128, rows // 128 * 128)
+    out = torch.empty((N, K), dtype=FP8, device=w.device)
     ws = torch.empty((N // 128, K // 128), dtype=torch.float32, device=w.device)
     for r0 in range(0, N, rows):
         r1 = min(N, r0 + rows)
         wf = w[r0:r1].float().view((r1 - r0) // 128, 128, K // 128, 128)
         scale = wf.abs().amax(dim=(1, 3), keepdim=True).clamp(min=1e-12) / 448.0
-        q[r0:r1] = (wf / scale).clamp(-448.0, 448.0).to(FP8).view(r1 - r0, K)
+        q = (wf / scale).clamp(-448.0, 448.0).to(FP8).view(r1 - r0, K)
+        shuffle_fp8_weight(q, out=out[r0:r1])
         ws[r0 // 128:r1 // 128] = scale.view((r1 - r0) // 128, K // 128)
-    return shuffle_fp8_weight(q), ws
+        del wf, q
+    return out, ws
 
 
 def moe_gemm_tiles(expert_ids: torch.Tensor, num_post_pad: torch.Tensor,
