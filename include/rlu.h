@@ -199,6 +199,21 @@ int rlu_moe_gemm_fp8blk_tiled_silu_quant(const void* qx, const float* xs, const 
                                          const int* ntiles, int max_tiles, void* q2, float* s2,
                                          int mtk, int top_k, int K, int N, hipStream_t stream);
 
+/* No counterpart in the reference (which runs the down GEMM into ic3 and then vLLM's moe_sum,
+ * r4d_mxfp4_moe.py.lru.diff:690-696): the decode down projection with moe_sum folded in.
+ * out[t] (bf16 [M, N]) = sum over k in k order, in float32, of bf16(down row (t, k) x
+ * topk_weights[t, k]) -- the values rlu_moe_gemm_split (sk = 1) writes into ic3 followed by
+ * rlu_moe_sum, bit for bit. q2 e4m3 [M top_k, K], s2 float [M top_k, K/128]; topk_ids int32
+ * [M, top_k] (every id in [0, E)); table int32 [E] (expert -> slot or -1, the cache state after
+ * this step's manager); expert e comes from slot table[e] of w_hot / s_hot when resident, else
+ * from w_full / s_full (device or pinned host memory), both in fragment order with 128x128
+ * block scales. Built for K = 768 and top_k = 10 (-6 otherwise); N % 64 == 0. Returns -1 / -2 /
+ * -6 or a HIP error code. */
+int rlu_moe_down_sum(const void* q2, const float* s2, const int* topk_ids,
+                     const float* topk_weights, const int* table, const void* w_hot,
+                     const float* s_hot, const void* w_full, const float* s_full, void* out,
+                     int M, int top_k, int K, int N, int E, hipStream_t stream);
+
 /* No counterpart in the reference. For callers that cannot allocate -- code recorded into a HIP
  * graph, serving loops and harnesses that forbid hipMalloc: rlu_moe_gemm_tiles followed by
  * rlu_moe_gemm_fp8blk_tiled (same kernels, same results bit for bit) with the tile list kept in

@@ -1,0 +1,155 @@
+// The decode down projection with moe_sum folded in, token-major: out[t] = sum over k of
+// bf16(down(q2[t top_k + k]) x tw[t, k]), summed in float32 in k order and rounded to bf16 --
+// the values rlu_moe_gemm_split (sk = 1) writes into ic3 followed by moe_sum_k, bit for bit,
+// without the [mtk, N] intermediate or the moe_sum launch.
+//
+// A workgroup owns one token and W x 16 output columns; wave w owns 16 of them and walks the
+// token's top_k experts in k order (top_k a compile-time constant: the loop is unrolled, so
+// the experts' addresses and routed weights sit in scalar registers, loaded up front). Per expert it runs the K steps of the grouped GEMM for the
+// token's A rows (one MFMA per step: 16 rows x 16 columns, of which row k is the one kept) with
+// the same per-step fma as moe_gemm_k, multiplies by the routed weight, rounds to bf16 and adds
+// the value into the running sum. The token's activation fragments for every K step are loaded
+// once and serve all top_k experts; the weights stream through a ring of NS stages (one
+// expert's K range) that runs on across experts, so expert k + 1's strip is in flight while
+// expert k is summed. Experts come from the layer's cache table: a resident expert from its
+// slot, any other from the full tensor (device or pinned host memory).
+//
+// Each expert strip is read once per token that routes to it; workgroups are laid out so that
+// the tokens of one column range run on one XCD at the same time and share its L2.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "gemm_common.h"
+#include "numerics.h"
+#include "wave.h"
+
+namespace rlu {
+namespace dsum {
+
+constexpr int NXCD = 8;
+constexpr int BUF_WORD3 = 0x00020000;      // raw buffer descriptor word 3 on gfx9 (no format)
+constexpr int NTP = 2;                     // buffer cache policy: streaming
+constexpr int MAXK = 16;                   // top_k the kernel takes (A rows of one MFMA)
+
+template <int NS, int W, int TK>
+__global__ __launch_bounds__(W * WAVE) void down_sum_k(
+    const uint8_t* __restrict__ qa, const float* __restrict__ sa, const int* __restrict__ ids,
+    const float* __restrict__ tw, const int* __restrict__ table,
+    const uint8_t* __restrict__ hw, const float* __restrict__ hs,
+    const uint8_t* __restrict__ cw, const float* __restrict__ cs,
+    uint16_t* __restrict__ out, int M, int N, int E) {
+  constexpr int K = NS * 128;
+  static_assert(TK <= MAXK, "top_k rows fit one MFMA");
+  const int lane = lane_id(), w = uniform((int)(threadIdx.x / WAVE));
+  const int r16 = lane & 15, c4 = lane >> 4;
+  // workgroup -> (token, column group): the tokens of one column group are consecutive within
+  // an XCD's share of the grid (workgroup b runs on XCD b % 8)
+  const int ncg = N / (16 * W);
+  const int G = (int)gridDim.x;
+  const int nx = G % NXCD == 0 ? NXCD : 1;
+  const int pos = ((int)blockIdx.x % nx) * (G / nx) + (int)blockIdx.x / nx;
+  const int cg = pos / M, t = pos - cg * M;
+  const int col0 = (cg * W + w) * 16;
+
+  // the token's experts (scalar loads, all up front) and where each one's weights live
+  const uint8_t* wp[TK];
+  const float* sp[TK];
+  float twk[TK];
+#pragma unroll
+  for (int k = 0; k < TK; ++k) {
+    int e = ids[t * TK + k];
+    e = e < 0 || e >= E ? 0 : e;
+    const int s = table[e];
+    wp[k] = (s >= 0 ? hw + (size_t)s * N * K : cw + (size_t)e * N * K) + (size_t)col0 * K;
+    sp[k] = (s >= 0 ? hs + (size_t)s * (N / 128) * NS : cs + (size_t)e * (N / 128) * NS) +
+            (size_t)(col0 / 128) * NS;
+    twk[k] = tw[t * TK + k];
+  }
+  // the token's A rows: row r16 of the MFMA is (t, k = r16); rows past top_k repeat row 0
+  const int arow = t * TK + (r16 < TK ? r16 : 0);
+  v4u ra[NS][2];
+#pragma unroll
+  for (int j = 0; j < NS; ++j) {
+    const uint8_t* p = qa + (size_t)arow * K + j * 128 + 16 * c4;
+    ra[j][0] = *reinterpret_cast<const v4u*>(p);
+    ra[j][1] = *reinterpret_cast<const v4u*>(p + 64);
+  }
+  v4u rb[NS][2];
+  const int voff = lane * 16;
+  auto issue = [&](int j, __amdgpu_buffer_rsrc_t b) __attribute__((always_inline)) {
+    rb[j][0] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(b, voff, j * 2048, NTP));
+    rb[j][1] = __builtin_bit_cast(
+        v4u, __builtin_amdgcn_raw_buffer_load_b128(b, voff + 1024, j * 2048, NTP));
+  };
+  auto wbuf = [&](int k) __attribute__((always_inline)) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)wp[k < TK ? k : TK - 1], 0,
+                                             k < TK ? 16 * K : 0, BUF_WORD3);
+  };
+  // expert k's per-step scales (activation row (t, k) x weight block), vector loads issued one
+  // expert ahead, so waiting for them waits only for weight loads already consumed
+  float fx[2][NS], fw[2][NS];
+  auto load_scales = [&](int k, int q) __attribute__((always_inline)) {
+    const int kk = k < TK ? k : TK - 1;
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+      fx[q][j] = sa[(size_t)(t * TK + kk) * NS + j];
+      fw[q][j] = sp[kk][j];
+    }
+  };
+  load_scales(0, 0);
+#pragma unroll
+  for (int j = 0; j < NS; ++j) issue(j, wbuf(0));
+  float sum = 0.f;
+#pragma unroll
+  for (int k = 0; k < TK; ++k) {
+    const int q = k & 1;
+    load_scales(k + 1, q ^ 1);
+    const __amdgpu_buffer_rsrc_t bn = wbuf(k + 1);
+    v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+      const float f = fx[q][j] * fw[q][j];
+      const v4f d = mfma_f8(pack8(ra[j][0], ra[j][1]), pack8(rb[j][0], rb[j][1]));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] = fmaf(d[i], f, acc[i]);
+      asm volatile("" : "+v"(acc));
+      issue(j, bn);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // row k sits in lanes c4 = k / 4, element k % 4: round it as the GEMM epilogue does, move
+    // it to the lanes of c4 = 0 and add it in k order
+    const float y = bf16_to_f32(f32_to_bf16(acc[k & 3] * twk[k]));
+    sum = __fadd_rn(sum, __shfl(y, r16 + 16 * (k >> 2)));
+  }
+  if (c4 == 0) out[(size_t)t * N + col0 + r16] = f32_to_bf16(sum);
+}
+
+}  // namespace dsum
+}  // namespace rlu
+
+extern "C" {
+
+// No counterpart in the reference, which runs the down GEMM into ic3 and then vLLM's moe_sum
+// (r4d_mxfp4_moe.py.lru.diff:690-696). See include/rlu.h.
+int rlu_moe_down_sum(const void* q2, const float* s2, const int* topk_ids,
+                     const float* topk_weights, const int* table, const void* w_hot,
+                     const float* s_hot, const void* w_full, const float* s_full, void* out,
+                     int M, int top_k, int K, int N, int E, hipStream_t stream) {
+  using namespace rlu;
+  if (M < 0 || top_k < 1 || top_k > dsum::MAXK || K <= 0 || N <= 0 || E <= 0) return -1;
+  if (!q2 || !s2 || !topk_ids || !topk_weights || !table || !w_full || !s_full || !out)
+    return -1;
+  if (K % 128 || N % 128) return -2;
+  if (K != 768 || top_k != 10) return -6;          // built for the 768-deep down, top-10
+  if (N % 64) return -2;
+  if (M == 0) return 0;
+  constexpr int W = 4;
+  const int grid = M * (N / (16 * W));
+  hipLaunchKernelGGL((dsum::down_sum_k<6, W, 10>), dim3(grid), dim3(W * WAVE), 0, stream,
+                     (const uint8_t*)q2, s2, topk_ids, topk_weights, table,
+                     (const uint8_t*)w_hot, s_hot, (const uint8_t*)w_full, s_full,
+                     (uint16_t*)out, M, N, E);
+  return (int)hipGetLastError();
+}
+
+}  // extern "C"

@@ -28,6 +28,11 @@ BLOCK = 16
 # Routed rows (tokens x top_k) from which a layer runs the tiled (prefill) grouped GEMM instead
 # of the decode one: a 2048-token chunk at top-10 gives 20480, ~40 rows per expert over 512.
 PREFILL_ROWS = 2048
+# Tokens up to which a decode step folds moe_sum into the down projection (ops.moe_down_sum):
+# the token-major kernel reads each expert strip once per token routed to it, which pays at
+# B=1 (5 tokens: 16.3 vs 18.9 us per layer for down + moe_sum) and loses at B=4 (20 tokens:
+# 41.0 vs 22.9 us).
+FOLD_SUM_TOKENS = 8
 
 
 @dataclass
@@ -57,7 +62,7 @@ class LruMoELayer:
                  top_k: int, device="cuda", slots: ExpertWeights | None = None,
                  npw1: int = 2, npw2: int = 4, sk1: int | None = None, sk2: int = 1,
                  wv: int = 0, max_inserts: int | None = None,
-                 prefill_rows: int = PREFILL_ROWS):
+                 prefill_rows: int = PREFILL_ROWS, fold_sum: bool | None = None):
         """npw / sk: 16-column tiles per item and K split of gate_up (1) and down (2); the
         defaults are the fastest measured at the decode shapes (hidden 2560, intermediate
         768): gate_up splits K over 2 waves above 8 tokens (20 tokens: 3.70 vs 3.95 ms per
@@ -73,7 +78,12 @@ class LruMoELayer:
         once per tile) over the hot and the cold align, in place of the decode kernel; npw /
         sk / wv do not apply to it. Its output equals the decode kernel's with sk = 1 bit
         for bit. The reference runs prefill chunks through the same split path
-        (r4d_mxfp4_moe.py.lru.diff:659-696; tests/lru/test_numerics_prod.py:44-48)."""
+        (r4d_mxfp4_moe.py.lru.diff:659-696; tests/lru/test_numerics_prod.py:44-48).
+
+        fold_sum: run down and moe_sum as one token-major kernel (ops.moe_down_sum, the same
+        output bit for bit) when the gather is not overlapped; default on up to
+        FOLD_SUM_TOKENS tokens at the shapes the kernel is built for (intermediate 768,
+        top-10)."""
         dev = torch.device(device)
         self.full = full
         self.full_ptrs = full.ptrs()
@@ -110,6 +120,11 @@ class LruMoELayer:
         self.qx = torch.empty((self.M, self.H), dtype=ops.FP8, device=dev)
         self.xs = torch.empty((self.M, self.H // 128), dtype=torch.float32, device=dev)
         self.prefill = self.mtk >= prefill_rows
+        if fold_sum is None:
+            fold_sum = (not self.prefill and max_tokens <= FOLD_SUM_TOKENS and self.I == 768
+                        and top_k == 10)
+        self.fold_sum = fold_sum
+        self.ids32 = torch.empty((self.M, top_k), dtype=torch.int32, device=dev)
         # prefill gate_up with SiLU-mul-quant in its epilogue where a kernel is built for the
         # shape: no [mtk, 2I] bf16 intermediate (same q2 / s2 bits)
         self.fuse_act = self.prefill and ops.moe_gemm_tiled_silu_quant_built(self.H, self.N1)
@@ -286,5 +301,14 @@ class LruMoELayer:
             if waited is not None:
                 torch.cuda.current_stream().wait_stream(waited)
             self._gate_up_act()
+            if self.fold_sum:
+                ids = topk_ids
+                if ids.dtype != torch.int32 or not ids.is_contiguous():
+                    self.ids32.copy_(ids)
+                    ids = self.ids32
+                ops.moe_down_sum(self.q2, self.s2, ids, tw.view(M, self.top_k),
+                                 self.cache.table, self.slots.w2, self.slots.s2, self.full.w2,
+                                 self.full.s2, output)
+                return
             self._gemm_split(*down, 2, tw, 1, self.npw2, self.sk2)
         ops.moe_sum(self.ic3.view(M, self.top_k, self.H), output)

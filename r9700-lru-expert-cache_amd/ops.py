@@ -89,6 +89,27 @@ def moe_sum(ic3: torch.Tensor, output: torch.Tensor) -> None:
     check(rc, "rlu_moe_sum")
 
 
+def moe_down_sum(q2: torch.Tensor, s2: torch.Tensor, topk_ids: torch.Tensor,
+                 topk_weights: torch.Tensor, table: torch.Tensor, w_hot: torch.Tensor,
+                 s_hot: torch.Tensor, w_full: torch.Tensor, s_full: torch.Tensor,
+                 out: torch.Tensor) -> None:
+    """The decode down projection with moe_sum folded in: out [M, N] bf16 = moe_sum of the
+    down GEMM's routed-weight rows, bit for bit, without the [M top_k, N] intermediate. Expert
+    e comes from slot table[e] of (w_hot, s_hot) when resident, else from (w_full, s_full)
+    (device or pinned host memory). topk_ids int32 [M, top_k] with every id in [0, E)."""
+    M, top_k = topk_ids.shape
+    N, K = w_full.shape[1], w_full.shape[2]
+    assert topk_ids.dtype == torch.int32 and topk_ids.is_contiguous()
+    assert topk_weights.dtype == torch.float32 and topk_weights.is_contiguous()
+    assert topk_weights.shape == (M, top_k) and q2.shape == (M * top_k, K)
+    assert out.shape == (M, N) and out.dtype == torch.bfloat16 and out.is_contiguous()
+    rc = lib().rlu_moe_down_sum(
+        _p(q2), _p(s2), _p(topk_ids), _p(topk_weights), _p(table), _p(w_hot), _p(s_hot),
+        _P(device_ptr(w_full)), _P(device_ptr(s_full)), _p(out), M, top_k, K, N,
+        w_full.shape[0], _P(stream_ptr()))
+    check(rc, "rlu_moe_down_sum")
+
+
 def _r4d_fp8_moe_gemm_into(y: torch.Tensor, qx: torch.Tensor, x_scale: torch.Tensor,
                            wq: torch.Tensor, ws_t: torch.Tensor, wref: torch.Tensor | None,
                            sorted_ids: torch.Tensor, expert_ids: torch.Tensor,

@@ -466,6 +466,77 @@ def test_moe_gemm_split_one_launch_equals_two_calls(pkg, ops, layer):
     assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
 
 
+# ---- down + moe_sum folded (decode) ----------------------------------------------------------
+@pytest.mark.parametrize("M,pinned", [(1, False), (5, False), (20, False), (20, True)])
+def test_moe_down_sum_equals_split_gemm_and_moe_sum(pkg, ops, layer, M, pinned):
+    """The token-major down + moe_sum equals the split down GEMM (hot slots + cold full
+    tensor, sk = 1) into ic3 followed by moe_sum, bit for bit; the cold experts come from the
+    full tensor in device or pinned host memory."""
+    E, H, I = layer["E"], layer["H"], layer["I"]
+    top_k = 10
+    ids = routing(M, top_k, E, seed=M + 91)
+    mtk = ids.size
+    hot_experts = sorted(set(ids.reshape(-1).tolist()))[1::2]
+    hot = {ex: i for i, ex in enumerate(hot_experts)}
+    sh, eh, nh, sc, ec, nc = align_all(ids, E, hot)
+    table = np.full(E, -1, np.int32)
+    for ex, sl in hot.items():
+        table[ex] = sl
+    sq = layer["w2t"][torch.tensor(hot_experts, device=DEV)].contiguous()
+    ss = layer["w2s"][torch.tensor(hot_experts, device=DEV)].contiguous()
+    if pinned:
+        fq = torch.empty(layer["w2t"].shape, dtype=layer["w2t"].dtype, pin_memory=True)
+        fq.copy_(layer["w2t"])
+        fs = torch.empty(layer["w2s"].shape, dtype=torch.float32, pin_memory=True)
+        fs.copy_(layer["w2s"])
+    else:
+        fq, fs = layer["w2t"], layer["w2s"]
+    rng = np.random.default_rng(M + 91)
+    a = fp8.bf16_round(rng.standard_normal((mtk, I)).astype(np.float32))
+    q2, s2 = fp8.group_quant(a, 128)
+    q2_t = torch.from_numpy(q2).to(DEV).view(torch.float8_e4m3fn)
+    s2_t = torch.from_numpy(s2).to(DEV)
+    tw = torch.from_numpy(rng.random((M, top_k)).astype(np.float32)).to(DEV)
+    al = to_dev_i32(sh, eh, nh, sc, ec, nc)
+    from importlib import import_module
+    moe = import_module(pkg.__name__ + ".moe")
+    P = ctypes.c_void_p
+    fqp = moe.device_ptr_of_pinned(fq) if pinned else fq.data_ptr()
+    fsp = moe.device_ptr_of_pinned(fs) if pinned else fs.data_ptr()
+    ic3 = torch.full((mtk, H), float("nan"), dtype=torch.bfloat16, device=DEV)
+    gpu_case(f"down + moe_sum unfused M={M} pinned={pinned}")
+    rc = pkg.lib().rlu_moe_gemm_split(
+        P(q2_t.data_ptr()), P(s2_t.data_ptr()), P(sq.data_ptr()), P(ss.data_ptr()),
+        P(al[0].data_ptr()), P(al[1].data_ptr()), P(al[2].data_ptr()), P(fqp), P(fsp),
+        P(al[3].data_ptr()), P(al[4].data_ptr()), P(al[5].data_ptr()), P(tw.data_ptr()),
+        P(ic3.data_ptr()), al[0].numel(), mtk, 1, I, H, 0, 1, 4,
+        P(torch.cuda.current_stream().cuda_stream))
+    assert rc == 0
+    want = torch.empty((M, H), dtype=torch.bfloat16, device=DEV)
+    ops.moe_sum(ic3.view(M, top_k, H), want)
+    got = torch.full((M, H), float("nan"), dtype=torch.bfloat16, device=DEV)
+    gpu_case(f"down + moe_sum folded M={M} pinned={pinned}")
+    ops.moe_down_sum(q2_t, s2_t, torch.from_numpy(ids.astype(np.int32)).to(DEV), tw,
+                     torch.from_numpy(table).to(DEV), sq, ss, fq, fs, got)
+    torch.cuda.synchronize()
+    assert not torch.isnan(ic3).any()
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+def test_moe_down_sum_return_codes(pkg):
+    """Argument errors return before anything is launched."""
+    P = ctypes.c_void_p
+    f = pkg.lib().rlu_moe_down_sum
+    x = torch.empty(1 << 16, dtype=torch.uint8, device=DEV)
+    p = P(x.data_ptr())
+    s = P(torch.cuda.current_stream().cuda_stream)
+    assert f(p, p, p, p, p, p, p, p, p, p, 4, 10, 1024, 2560, 64, s) == -6
+    assert f(p, p, p, p, p, p, p, p, p, p, 4, 8, 768, 2560, 64, s) == -6
+    assert f(p, p, p, p, p, p, p, p, p, p, 4, 17, 768, 2560, 64, s) == -1
+    assert f(p, p, p, p, p, p, p, p, p, p, 4, 10, 768, 2500, 64, s) == -2
+    assert f(P(0), p, p, p, p, p, p, p, p, p, 4, 10, 768, 2560, 64, s) == -1
+
+
 # ---- the tiled (prefill) grouped GEMM ---------------------------------------------------------
 def tiles_ref(eids, npad, tmb=8):
     """The tile list by walking the align output: each run of one expert's blocks cut into
