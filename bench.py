@@ -18,6 +18,12 @@ GEMM); the same step at B=1 (5 tokens) is `b1_ms_per_step`, with the gather
 `b1_e2e_with_gather_ms_per_step`. The
 static hot/cold arm (inserts disabled: the warm-start set stays resident and every other
 routed expert is read over PCIe by the GEMMs, every step) is `e2e_static_arm_ms_per_step`.
+`pcie_mb_per_step` counts the host-link bytes of both arms (experts inserted + distinct routed
+experts left cold, from the device state after each step) on this trace and on routing drawn
+from the reference's hot profile (`profile_trace`: tests/golden/hot_profile.json).
+`step_frac` is the grouped GEMMs' algorithmic bytes of a step over `ms_per_step`, as a fraction
+of 8 TB/s. `prefill_4096` times the prefill kernels on a 4096-token chunk; `cpu_baseline` the
+layer step in torch fp32 on the host cores.
 
     python bench.py [--steps K] [--warmup W] [--only-b4]
 """
