@@ -349,3 +349,67 @@ def test_layer_prefill_read_through(pkg, pool):
         ref = oracle_layer(x[pick], ids[pick], tw[pick], pool)
         err = ogemm.rel_err(oa.float().cpu().numpy()[pick], ref)
         assert err <= TOL, f"step {t}: rel err {err:.3e}"
+
+
+def test_layer_prefill_graph_replay(pkg, pool):
+    """A prefill-sized step (256 tokens, 2560 routed rows: the tiled kernels, gate_up with the
+    activation in its epilogue) captured once as a HIP graph with the overlapped gather and
+    replayed with new routing -- alternately wide (read-through) and narrow (10 experts to
+    install) -- equals an eager layer without the overlap, bit for bit, output and state."""
+    M, steps = 256, 5
+    _, perm0 = trace.zipf_trace(seed=610, E=E, rows=20, k=TOPK, steps=1, s=1.1)
+    hot, rank = trace.warm_hot(perm0, S)
+    full = pkg.ExpertWeights(pool["w13"], pool["w13s"], pool["w2"], pool["w2s"])
+    a = pkg.LruMoELayer(full, hot, rank, M, TOPK, DEV)
+    b = pkg.LruMoELayer(full, hot, rank, M, TOPK, DEV)
+    assert a.prefill and a.fuse_act
+    rng = np.random.default_rng(610)
+    hs = set(int(e) for e in hot)
+    cold = [e for e in range(E) if e not in hs]
+    ids_all = []
+    for t in range(steps):
+        if t % 2:
+            pool_ids = np.array(sorted(rng.choice(sorted(hs), 20, replace=False).tolist()
+                                       + rng.choice(cold, 10, replace=False).tolist()), np.int32)
+        else:
+            pool_ids = np.arange(E, dtype=np.int32)
+        ids_all.append(np.stack([rng.choice(pool_ids, TOPK, replace=False)
+                                 for _ in range(M)]).astype(np.int32))
+    xs = [torch.from_numpy(fp8.bf16_round(rng.standard_normal((M, H)).astype(np.float32)))
+          .to(torch.bfloat16).to(DEV) for _ in range(steps)]
+    tws = [torch.from_numpy(rng.random((M, TOPK)).astype(np.float32)).to(DEV)
+           for _ in range(steps)]
+    x_st, tw_st = torch.empty_like(xs[0]), torch.empty_like(tws[0])
+    ids_st = torch.empty((M, TOPK), dtype=torch.int32, device=DEV)
+    out_a = torch.empty((M, H), dtype=torch.bfloat16, device=DEV)
+    out_b = torch.empty_like(out_a)
+    side = torch.cuda.Stream()
+    gpu_case("prefill graph: eager step 0")
+    ids0 = torch.from_numpy(ids_all[0]).to(DEV)
+    a.apply(out_a, xs[0], tws[0], ids0, gather=True, side=side, overlap=True)
+    b.apply(out_b, xs[0], tws[0], ids0, gather=True, side=side, overlap=False)
+    torch.cuda.synchronize()
+    assert torch.equal(out_a.view(torch.int16), out_b.view(torch.int16))
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        a.apply(out_a, x_st, tw_st, ids_st, gather=True, side=side, overlap=True)
+    torch.cuda.synchronize()
+    installs = 0
+    for t in range(1, steps):
+        gpu_case(f"prefill graph: replay step {t}")
+        ids = torch.from_numpy(ids_all[t]).to(DEV)
+        x_st.copy_(xs[t])
+        tw_st.copy_(tws[t])
+        ids_st.copy_(ids)
+        g.replay()
+        b.apply(out_b, xs[t], tws[t], ids, gather=True, side=side, overlap=False)
+        torch.cuda.synchronize()
+        installs += int(a.cache.n_miss.item())
+        assert not torch.isnan(out_a).any()
+        assert torch.equal(out_a.view(torch.int16), out_b.view(torch.int16)), f"replay {t}"
+        for name, ga, gb in zip(olru.LruState.NAMES, a.cache.state(), b.cache.state()):
+            assert torch.equal(ga, gb), (t, name)
+        out_a.zero_()                       # eager work between replays
+        torch.cuda.synchronize()
+    assert installs > 0, "the narrow steps must install experts"
+    del g
