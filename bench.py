@@ -89,21 +89,25 @@ def make_pool(torch, dev, ops):
     return out
 
 
-def layer_trace(layer, rows, steps):
+def layer_trace(layer, rows, steps, corr=None):
+    """The layer's Zipf(1.1) routing; rows correlated at 20 rows by default (corr 0.7: 5-13
+    misses per layer per step, about 47 distinct experts), uncorrelated with corr=0 (about 97
+    distinct at 20 rows)."""
     trace = load_pkg().traces
-    corr = 0.7 if rows >= 20 else 0.0
+    if corr is None:
+        corr = 0.7 if rows >= 20 else 0.0
     return trace.zipf_trace(seed=1000 + layer, E=E, rows=rows, k=TOPK, steps=steps, s=1.1,
                             corr=corr)
 
 
 def build(torch, pkg, rows, steps, dev, pool_dev, host_full, layers_cache=None,
-          max_inserts=None):
+          max_inserts=None, corr=None):
     """Layers (slots shared between batch sizes: the hot set depends only on the layer seed)."""
     trace = pkg.traces
     ids = np.empty((steps, LAYERS, rows, TOPK), np.int32)
     layers = []
     for l in range(LAYERS):
-        tr, perm0 = layer_trace(l, rows, steps)
+        tr, perm0 = layer_trace(l, rows, steps, corr)
         ids[:, l] = tr.reshape(steps, rows, TOPK)
         hot, rank = trace.warm_hot(perm0, S)
         if layers_cache is not None and l < len(layers_cache):
@@ -377,10 +381,13 @@ def prefill_gemm(torch, pkg, dev, T=4096, reps=3, lru=True, wv=0):
     tiles = torch.empty(2 * eh.numel() + 1, dtype=torch.int32, device=dev)
 
     def timed(fn):
+        # each timed call starts from an idle GPU: these kernels draw enough power that a few
+        # ms of them back to back lower the clocks, which spreads repeated timings by 10-20%
         fn()
         torch.cuda.synchronize()
         best = 1e30
         for _ in range(reps):
+            time.sleep(0.1)
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             a.record()
             fn()
@@ -968,6 +975,28 @@ def main():
             float(np.mean([int(L.cache.n_miss.item()) for L in layers1])), 2)
         log(f"B=1 with PCIe miss gather: {ms1e:.3f} ms")
         del g1e, layers1
+        torch.cuda.synchronize()
+        # B=4, HBM-resident, on the uncorrelated trace (about twice the distinct experts)
+        layersU, idsU = build(torch, pkg, rows4, args.warmup + args.steps + 2, dev, pool,
+                              host_full, layers_cache=layers4, corr=0.0)
+        idsU_dev = torch.from_numpy(idsU).to(dev)
+        idsU_static = torch.empty_like(idsU_dev[0])
+        idsU_static.copy_(idsU_dev[0])
+        gU = capture(torch, layersU, idsU_static, tw4, hb4, gather=False, side=side)
+        run_steps(torch, gU, idsU_dev, idsU_static, 0, args.warmup)
+        msU, _ = time_steps(torch, gU, idsU_dev, idsU_static, args.warmup, args.steps)
+        rU = gemm_roofline(torch, pkg, layersU, idsU[args.warmup + args.steps - 1], rows4)
+        stepU = rU["algorithmic_bytes_per_launch"] * 2 * LAYERS
+        out["b4_uncorrelated"] = {
+            "routing": "the same Zipf(1.1) layers with uncorrelated rows (corr 0)",
+            "ms_per_step": round(msU, 4),
+            "distinct_experts_per_layer": rU["distinct_experts_per_layer"],
+            "avg_launch_us": rU["avg_launch_us"], "achieved": rU["achieved"],
+            "frac": rU["frac"],
+            "step_frac": round(stepU / (msU * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        log(f"B=4 uncorrelated routing: {msU:.3f} ms, {rU['distinct_experts_per_layer']} "
+            f"distinct, GEMM frac {rU['frac']}")
+        del gU, layersU
         torch.cuda.synchronize()
         # B=4 with routing from the reference's hot profile, LRU and static arms, gather on
         TP = args.warmup + 2 * args.steps + 2 + PCIE_STEPS
