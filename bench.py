@@ -441,6 +441,20 @@ def prefill_gemm(torch, pkg, dev, T=4096, reps=3, lru=True, wv=0):
     res["kernel"] = "streamed prefill kernel" if wv == 0 else f"tiled_k, {wv} workgroups/CU"
     res["tokens"], res["rows_per_expert"] = T, round(mtk / E, 1)
     res["tiles"] = int(tiles[-1].item())
+    if lru:
+        # the whole layer step on this chunk: every expert resident (the slots are the weight
+        # tensors themselves), apply() without a gather. Uniform routing over 512 experts is a
+        # read-through step (512 distinct > 256), so repeated steps leave the cache as it is.
+        full = pkg.ExpertWeights(w13, w13s, w2, w2s)
+        layer = pkg.LruMoELayer(full, range(E), None, T, TOPK, dev, slots=full)
+        ids_t = torch.from_numpy(ids).to(dev)
+        twl = torch.rand(T, TOPK, device=dev, generator=g)
+        out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+        res["layer_step_us"] = round(timed(lambda: layer.apply(out, hs, twl, ids_t,
+                                                                 gather=False)), 1)
+        res["layer_step"] = ("LruMoELayer.apply on the chunk: fused LRU + align + quant, gate_up "
+                             "with SiLU-mul-quant, down, moe_sum")
+        del layer
     del w13, w2
     torch.cuda.empty_cache()
     return res
