@@ -121,8 +121,11 @@ class LruMoELayer:
         self.xs = torch.empty((self.M, self.H // 128), dtype=torch.float32, device=dev)
         self.prefill = self.mtk >= prefill_rows
         if fold_sum is None:
+            # not for the static arm: its cold experts are the common case, and the folded
+            # kernel reads an expert's strip once per token routed to it -- over the host
+            # link for a cold one
             fold_sum = (not self.prefill and max_tokens <= FOLD_SUM_TOKENS and self.I == 768
-                        and top_k == 10)
+                        and top_k == 10 and self.cache.max_inserts > 0)
         self.fold_sum = fold_sum
         self.ids32 = torch.empty((self.M, top_k), dtype=torch.int32, device=dev)
         # prefill gate_up with SiLU-mul-quant in its epilogue where a kernel is built for the
