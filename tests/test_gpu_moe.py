@@ -537,6 +537,62 @@ def test_moe_down_sum_return_codes(pkg):
     assert f(P(0), p, p, p, p, p, p, p, p, p, 4, 10, 768, 2560, 64, s) == -1
 
 
+# ---- a tensor-parallel rank's shapes ----------------------------------------------------------
+@pytest.mark.parametrize("which", ["gate_up", "down"])
+def test_moe_gemm_tp2_shapes(ops, which):
+    """One rank of tensor parallel 2 (intermediate 768 / 2 = 384): gate_up [768, 2560] and
+    down [2560, 384] on the decode kernel (every sk it takes at that K) within 1e-2 of the
+    float64 oracle, and on the prefill kernel (gate_up: the streamed kernel at N = 768; down:
+    no streamed configuration at K = 384, so the general tiled kernel) bit-identical to the
+    decode kernel at sk = 1. gate_up's SiLU-mul-quant epilogue (N = 768 is a multiple of 256)
+    equals silu_mul_quant of that output bit for bit."""
+    E, top_k = 24, 10
+    N, K = (768, 2560) if which == "gate_up" else (2560, 384)
+    wq, ws = make_experts(E, N, K, 11 if which == "gate_up" else 12)
+    wt = ops.shuffle_fp8_weight(wq)
+    for M in (5, 96):
+        ids = routing(M, top_k, E, seed=M + 41)
+        mtk = ids.size
+        al = align_all(ids, E)
+        rows = M if which == "gate_up" else mtk
+        tk = top_k if which == "gate_up" else 1
+        rng = np.random.default_rng(M + 41)
+        x = fp8.bf16_round(rng.standard_normal((rows, K)).astype(np.float32))
+        qx, xs = fp8.group_quant(x, 128)
+        qx_t = torch.from_numpy(qx).to(DEV).view(torch.float8_e4m3fn)
+        xs_t = torch.from_numpy(xs).to(DEV)
+        tw = None if which == "gate_up" else rng.random(mtk).astype(np.float32)
+        tw_t = None if tw is None else torch.from_numpy(tw).to(DEV)
+        used = sorted(set(ids.reshape(-1).tolist()))
+        wr, wsr = ref_from(wq, ws, used)
+        want = ogemm.moe_gemm(qx, xs, _Lazy(wr), _Lazy(wsr), *al, mtk, tk, tw=tw)
+        al_t = to_dev_i32(*al)
+        outs = {}
+        for sk in (1,) if K == 384 else (1, 2, 4):
+            y = torch.full((mtk, N), float("nan"), dtype=torch.bfloat16, device=DEV)
+            gpu_case(f"tp2 {which} M={M} decode sk={sk}")
+            run_gemm(ops, y, qx_t, xs_t, wt, ws, al_t, tw_t, mtk, tk, npw=2, sk=sk)
+            torch.cuda.synchronize()
+            err = ogemm.rel_err(np_from_bf16(y), want)
+            assert err <= TOL, f"{which} M={M} sk={sk}: rel err {err:.3e}"
+            outs[sk] = y
+        yt = torch.full((mtk, N), float("nan"), dtype=torch.bfloat16, device=DEV)
+        gpu_case(f"tp2 {which} M={M} prefill kernel")
+        ops.moe_gemm_tiled(yt, qx_t, xs_t, wt, ws, *al_t, tw_t, mtk, tk)
+        torch.cuda.synchronize()
+        assert torch.equal(yt.view(torch.int16), outs[1].view(torch.int16))
+        if which == "gate_up":
+            assert ops.moe_gemm_tiled_silu_quant_built(K, N)
+            _, q_ref, s_ref = ops.silu_mul_quant(yt)
+            q = torch.full((mtk, N // 2), 0x7F, dtype=torch.uint8, device=DEV).view(ops.FP8)
+            sc = torch.full((mtk, N // 256), float("nan"), device=DEV)
+            gpu_case(f"tp2 gate_up M={M} prefill kernel + silu-mul-quant")
+            ops.moe_gemm_tiled_silu_quant(q, sc, qx_t, xs_t, wt, ws, *al_t, mtk, tk)
+            torch.cuda.synchronize()
+            assert torch.equal(q.view(torch.uint8), q_ref.view(torch.uint8))
+            assert torch.equal(sc.view(torch.int32), s_ref.view(torch.int32))
+
+
 # ---- the tiled (prefill) grouped GEMM ---------------------------------------------------------
 def tiles_ref(eids, npad, tmb=8):
     """The tile list by walking the align output: each run of one expert's blocks cut into
