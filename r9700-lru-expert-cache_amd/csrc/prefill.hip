@@ -22,10 +22,11 @@
 //     anyway (the vector-memory counter retires in order). One barrier per chunk.
 //   * The activation scales of the chunk ride with it (LDS), the weight-block scales of an
 //     item come through scalar loads, and the routed weights and row ids of the next item are
-//     staged with its first chunk, so the epilogue reads LDS only. The epilogue stages the
-//     tile's bf16 outputs in the activation buffer its last chunk freed and writes each row
-//     with 16-byte nontemporal stores (the rows are scattered and not read again here; kept
-//     out of L2 they leave it to the weight stream -- about 50 us of 430 at 4096 tokens).
+//     staged with its first chunk, so the epilogue reads LDS only. In the epilogue each wave
+//     turns its own strips' bf16 outputs into 16-byte row pieces through a small LDS area of
+//     its own and stores them nontemporally (the rows are scattered and not re-read here;
+//     kept out of L2 they leave it to the weight stream), with no workgroup barrier, so a
+//     wave that finishes early starts the next item, whose weights are already in flight.
 //   * Item metadata (tile, expert) is read through scalar loads two items ahead, the next
 //     tile's sorted ids one item ahead.
 //   * Items go to XCDs in contiguous ranges of tiles (workgroup b runs on XCD b % 8): the
@@ -72,6 +73,7 @@ struct Item {
   int b0, nbk, e, n0;
 };
 
+typedef unsigned v2u __attribute__((ext_vector_type(2)));
 
 
 template <int NK, int W, int S, int KC, int D, int BR = 1, int BG = 2>
@@ -94,8 +96,11 @@ struct Cfg {
   static constexpr int A_OFF = (SX + 2 * RW) * 4;
   static constexpr int A_BUF = TB * KC * 2 * 1024;           // [blk][ks][h][lane] x 16 B
   static_assert(A_BUF <= 65536, "an activation buffer must fit one ds offset range");
-  static constexpr size_t LDS = (size_t)A_OFF + 2 * A_BUF;
-  // blocks of bf16 outputs ([16 rows][C]) one activation buffer holds in the epilogue
+  // each wave's own epilogue staging: one block's [16 rows][S 16 columns] bf16
+  static constexpr int EPI_W = 16 * S * 16 * 2;
+  static constexpr int EPI_OFF = A_OFF + 2 * A_BUF;
+  static constexpr size_t LDS = (size_t)EPI_OFF + W * EPI_W;
+  // blocks of bf16 outputs ([16 rows][C]) one activation buffer holds in the ACT epilogue
   static constexpr int BP = A_BUF / (16 * C * 2) < TB ? A_BUF / (16 * C * 2) : TB;
   static_assert(BP >= 1, "an epilogue pass holds at least one block");
 };
@@ -346,12 +351,50 @@ __global__ __launch_bounds__(W * WAVE) void stream_k(
         if (c + 1 == NCH) write_rows(par ^ 1);
         __syncthreads();
       }
-      // epilogue through the activation buffer this item's last chunk used (free after the
-      // chunk-end barrier): each wave puts its bf16 outputs (x routed weight) into a
-      // [rows][C] tile, then the workgroup writes every live row's C columns with 16-byte
-      // stores -- whole cache lines, where per-lane 2-byte stores from the MFMA layout cost
-      // about a fifth of the kernel's time. Blocks go BP at a time when the tile does not fit.
-      {
+      // epilogue, plain GEMM: each wave writes its own S 16 columns, block by block, through
+      // its own LDS staging area -- the bf16 outputs (x routed weight) of one block as [16
+      // rows][S 16], read back as 16-byte row pieces, four consecutive lanes to a row -- with
+      // nontemporal stores (the rows are scattered and not re-read here; kept out of L2 they
+      // leave it to the weight stream). No workgroup barrier: a wave that finishes its strips
+      // goes on to the next item, whose weights its ring already holds, while the others
+      // still store. The row ids and routed weights read here were written before the
+      // chunk-end barrier that closed the previous item, and are rewritten only after the
+      // next item's first one.
+      if constexpr (!ACT) {
+        uint16_t* st = reinterpret_cast<uint16_t*>(smem + CF::EPI_OFF + w * CF::EPI_W);
+        const int cw = col0(mA.n0);
+        constexpr int RC = S * 2;                         // 16-byte pieces per staged row
+#pragma unroll
+        for (int bk = 0; bk < TB; ++bk) {
+          if (bk < mA.nbk) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float wt = twl[par * TB * 16 + bk * 16 + 4 * c4 + i];
+#pragma unroll
+              for (int s = 0; s < S; ++s)
+                st[(4 * c4 + i) * S * 16 + s * 16 + r16] = f32_to_bf16(acc[bk][s][i] * wt);
+            }
+            wave_lds_sync();
+#pragma unroll
+            for (int u0 = 0; u0 < 16 * RC; u0 += WAVE) {
+              const int u = u0 + lane;
+              if (16 * RC % WAVE == 0 || u < 16 * RC) {
+                const int rr = u / RC, ch = u - rr * RC;
+                const int so = rows[par * TB * 16 + bk * 16 + rr];
+                const v4u v = *reinterpret_cast<const v4u*>(st + rr * S * 16 + ch * 8);
+                if (so < mtk)
+                  __builtin_nontemporal_store(
+                      v, reinterpret_cast<v4u*>(y + (size_t)so * N + cw + ch * 8));
+              }
+            }
+            wave_lds_sync();
+          }
+        }
+      } else {
+        // epilogue, SiLU-mul-quant: through the activation buffer this item's last chunk used
+        // (free after the chunk-end barrier) each wave puts its bf16 outputs into a [rows][C]
+        // tile; then 16-lane groups take whole rows (128 gate + 128 up columns), one row each.
+        // Blocks go BP at a time when the tile does not fit.
         const int qlast = (par * NCH + NCH - 1) & 1;
         uint16_t* ot = reinterpret_cast<uint16_t*>(smem + CF::A_OFF + qlast * CF::A_BUF);
 #pragma unroll
@@ -364,53 +407,37 @@ __global__ __launch_bounds__(W * WAVE) void stream_k(
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                   const int rr = t * 16 + 4 * c4 + i;
-                  const float wt = twl[par * TB * 16 + bk * 16 + 4 * c4 + i];
 #pragma unroll
                   for (int s = 0; s < S; ++s)
-                    ot[rr * C + (w * S + s) * 16 + r16] = f32_to_bf16(acc[bk][s][i] * wt);
+                    ot[rr * C + (w * S + s) * 16 + r16] = f32_to_bf16(acc[bk][s][i]);
                 }
               }
             }
             __syncthreads();
             const int nr = ((mA.nbk < p0 + CF::BP ? mA.nbk : p0 + CF::BP) - p0) * 16;
-            if (ACT) {
-              // one 16-lane row group per output row, lane l on columns [8 l, 8 l + 8) of the
-              // item's 128-column group (nr is a multiple of 16, so every wave's four groups
-              // run the same trip count and the DPP reduction sees whole groups)
-              const int I = N / 2, g = mA.n0 / C, l16 = lane & 15;
-              for (int rr = (int)threadIdx.x / 16; rr < nr; rr += W * 4) {
-                float gv[8], uv[8], a[8];
-                unpack8_bf16(*reinterpret_cast<const uint4*>(ot + rr * C + 8 * l16), gv);
-                unpack8_bf16(*reinterpret_cast<const uint4*>(ot + rr * C + 128 + 8 * l16), uv);
-                uint32_t mx = 0;
+            // one 16-lane row group per output row, lane l on columns [8 l, 8 l + 8) of the
+            // item's 128-column group (nr is a multiple of 16, so every wave's four groups
+            // run the same trip count and the DPP reduction sees whole groups)
+            const int I = N / 2, g = mA.n0 / C, l16 = lane & 15;
+            for (int rr = (int)threadIdx.x / 16; rr < nr; rr += W * 4) {
+              float gv[8], uv[8], a[8];
+              unpack8_bf16(*reinterpret_cast<const uint4*>(ot + rr * C + 8 * l16), gv);
+              unpack8_bf16(*reinterpret_cast<const uint4*>(ot + rr * C + 128 + 8 * l16), uv);
+              uint32_t mx = 0;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                  a[j] = bf16_to_f32(f32_to_bf16(__fmul_rn(silu_bf16(gv[j]), uv[j])));
-                  mx = max(mx, abs_bits(a[j]));
-                }
-                const float sc = scale_of(row_max_u32(mx));
-                const uint2 qv = quant8(a, sc);
-                const int so = rows[par * TB * 16 + p0 * 16 + rr];
-                if (so < mtk) {
-                  typedef unsigned v2u __attribute__((ext_vector_type(2)));
-                  __builtin_nontemporal_store(
-                      v2u{qv.x, qv.y},
-                      reinterpret_cast<v2u*>(q2 + (size_t)so * I + g * 128 + 8 * l16));
-                  if (l16 == 0) __builtin_nontemporal_store(sc, s2 + (size_t)so * (I / 128) + g);
-                }
+              for (int j = 0; j < 8; ++j) {
+                a[j] = bf16_to_f32(f32_to_bf16(__fmul_rn(silu_bf16(gv[j]), uv[j])));
+                mx = max(mx, abs_bits(a[j]));
               }
-              __syncthreads();
-              continue;
-            }
-            constexpr int CH = C / 8;                     // 16-byte chunks per row
-            for (int u = (int)threadIdx.x; u < nr * CH; u += W * WAVE) {
-              const int rr = u / CH, ch = u - rr * CH;
+              const float sc = scale_of(row_max_u32(mx));
+              const uint2 qv = quant8(a, sc);
               const int so = rows[par * TB * 16 + p0 * 16 + rr];
-              // nontemporal: output rows are scattered and not re-read by this
-              // kernel, so they should not displace the weight strips in L2
-              if (so < mtk)
-                __builtin_nontemporal_store(*reinterpret_cast<const v4u*>(ot + rr * C + ch * 8),
-                                            reinterpret_cast<v4u*>(y + (size_t)so * N + mA.n0 + ch * 8));
+              if (so < mtk) {
+                __builtin_nontemporal_store(
+                    v2u{qv.x, qv.y},
+                    reinterpret_cast<v2u*>(q2 + (size_t)so * I + g * 128 + 8 * l16));
+                if (l16 == 0) __builtin_nontemporal_store(sc, s2 + (size_t)so * (I / 128) + g);
+              }
             }
             __syncthreads();
           }
