@@ -358,7 +358,8 @@ def prefill_gemm(torch, pkg, dev, T=4096, reps=3, lru=True, wv=0):
     the fused LRU + align (read-through: 512 distinct > 128) and the prefill kernels (wv = 0:
     the streamed kernel at these shapes). Reports each GEMM's time, its dense TFLOP/s (2 mk N K)
     and its weight bytes / time; gate_up with SiLU-mul-quant in its epilogue (what the layer
-    runs) beside gate_up followed by the separate SiLU-mul-quant."""
+    runs) beside gate_up followed by the separate SiLU-mul-quant. The align's tile list is
+    built once (tile_list_us) and read by every GEMM, as the layer does."""
     ops = pkg.ops
     g = torch.Generator(device=dev).manual_seed(7)
     w13 = _fp8_bytes(torch, (E, 2 * I, H), dev, g)
@@ -395,17 +396,20 @@ def prefill_gemm(torch, pkg, dev, T=4096, reps=3, lru=True, wv=0):
             torch.cuda.synchronize()
             best = min(best, a.elapsed_time(b) * 1e3)
         return best
+    # the align's tile list, built once and read by both GEMMs (as the layer does)
+    u_tiles = timed(lambda: ops.moe_gemm_tiles(eh, nh, tiles))
     u1 = timed(lambda: ops.moe_gemm_tiled(y1, x, xs, w13, w13s, sh, eh, nh, None, mtk, TOPK,
-                                          tiles=tiles, wv=wv))
+                                          tiles=tiles, wv=wv, tiles_ready=True))
     u2 = timed(lambda: ops.moe_gemm_tiled(y2, x2, s2, w2, w2s, sh, eh, nh, tw, mtk, 1,
-                                          tiles=tiles, wv=wv))
+                                          tiles=tiles, wv=wv, tiles_ready=True))
     q2 = torch.empty(mtk, I, dtype=ops.FP8, device=dev)
     sq2 = torch.empty(mtk, I // 128, dtype=torch.float32, device=dev)
     u_act = timed(lambda: ops.silu_mul_quant(y1, out=(q2, sq2)))
     u_fused = None
     if wv == 0 and ops.moe_gemm_tiled_silu_quant_built(H, 2 * I):
         u_fused = timed(lambda: ops.moe_gemm_tiled_silu_quant(q2, sq2, x, xs, w13, w13s, sh, eh,
-                                                              nh, mtk, TOPK, tiles=tiles))
+                                                              nh, mtk, TOPK, tiles=tiles,
+                                                              tiles_ready=True))
     # the fused LRU + both aligns (+ the group-128 quant of the chunk's hidden states, as the
     # layer calls it) over the chunk's 40960 (token, k) ids
     ids_d = torch.from_numpy(ids).to(dev).reshape(-1)
@@ -431,6 +435,7 @@ def prefill_gemm(torch, pkg, dev, T=4096, reps=3, lru=True, wv=0):
         res[name] = dict(us=round(us, 1), tflops=round(2.0 * mtk * n * k / us / 1e6, 1),
                          weight_gbs=round(E * n * k / us / 1e3, 1))
     res["gate_up_plus_down_us"] = round(u1 + u2, 1)
+    res["tile_list_us"] = round(u_tiles, 1)
     res["silu_mul_quant_us"] = round(u_act, 1)
     if u_fused is not None:
         res["gate_up_silu_quant_fused_us"] = round(u_fused, 1)

@@ -138,10 +138,13 @@ class LruMoELayer:
         self.ic3 = torch.empty((self.mtk, self.H), dtype=torch.bfloat16, device=dev)
         self.tw = torch.empty((self.mtk,), dtype=torch.float32, device=dev)
         if self.prefill:
-            # the tile list of whichever align the next tiled call reads (calls are in
-            # stream order, so one list serves all of them)
-            self.tiles = torch.empty(2 * self.align[1].numel() + 1, dtype=torch.int32,
-                                     device=dev)
+            # one tile list per block-expert-id array the tiled GEMMs read (the hot align's,
+            # the cold align's, the overlap's two buckets), built by the first GEMM of a step
+            # that reads it and reused by the rest of that step
+            self.tiles = {t.data_ptr(): torch.empty(2 * t.numel() + 1, dtype=torch.int32,
+                                                    device=dev)
+                          for t in (self.align[1], self.align[4], self.eids_res, self.eids_new)}
+            self.tiles_built = set()
 
     @classmethod
     def from_profile(cls, full: ExpertWeights, profile, layer: int, budget_gb: float,
@@ -234,9 +237,18 @@ class LruMoELayer:
                                    top_k, self.wv, sk, npw)
 
     # -- the tiled (prefill) GEMM over one align ----------------------------------------------
+    def _tiles_of(self, eids, npad):
+        """The tile list of block expert ids eids, built on its first use in a step."""
+        key = eids.data_ptr()
+        ready = key in self.tiles_built
+        if not ready:
+            ops.moe_gemm_tiles(eids, npad, self.tiles[key])
+            self.tiles_built.add(key)
+        return self.tiles[key]
+
     def _gemm_tiled(self, y, qx, xs, w, s, sorted_ids, eids, npad, tw, top_k):
         ops.moe_gemm_tiled(y, qx, xs, w, s, sorted_ids, eids, npad, tw, y.shape[0], top_k,
-                           tiles=self.tiles)
+                           tiles=self._tiles_of(eids, npad), tiles_ready=True)
 
     # -- _act_quant: fused silu-and-mul + group-128 quant --------------------------------------
     def _act_quant(self):
@@ -251,7 +263,9 @@ class LruMoELayer:
                                                                nh)),) +
                              (((self.full.w13, self.full.s13, (sc, ec, nc)),) if cold else ())):
                 ops.moe_gemm_tiled_silu_quant(self.q2, self.s2, self.qx, self.xs, w, s, *al,
-                                              self.mtk, self.top_k, tiles=self.tiles)
+                                              self.mtk, self.top_k,
+                                              tiles=self._tiles_of(al[1], al[2]),
+                                              tiles_ready=True)
             return
         up = (self.ic1, self.qx, self.xs, self.slots.w13, self.slots.s13)
         if cold:
@@ -286,6 +300,8 @@ class LruMoELayer:
             overlap = self.cache.max_inserts > 0
         overlap = overlap and gather and side is not None
         waited = self._lru_step_fused(topk_ids, gather, side, hidden_states, split=overlap)
+        if self.prefill:
+            self.tiles_built.clear()                  # this step's aligns: lists rebuilt
         tw = topk_weights.reshape(-1)
         if tw.dtype != torch.float32 or not tw.is_contiguous():   # as fused_topk already gives
             self.tw.copy_(tw)

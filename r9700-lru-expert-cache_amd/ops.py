@@ -253,21 +253,31 @@ def moe_gemm_tiles(expert_ids: torch.Tensor, num_post_pad: torch.Tensor,
     return ws
 
 
+def _tile_list(expert_ids, num_post_pad, tiles, ready):
+    if ready:
+        assert tiles is not None and tiles.numel() == 2 * expert_ids.numel() + 1 \
+            and tiles.dtype == torch.int32, "tiles_ready needs the align's tile list"
+        return tiles
+    return moe_gemm_tiles(expert_ids, num_post_pad, tiles)
+
+
 def moe_gemm_tiled(y: torch.Tensor, qx: torch.Tensor, x_scale: torch.Tensor, wq: torch.Tensor,
                    ws_t: torch.Tensor, sorted_ids: torch.Tensor, expert_ids: torch.Tensor,
                    num_post_pad: torch.Tensor, topk_weights: torch.Tensor | None, mtk: int,
-                   top_k: int, tiles: torch.Tensor | None = None, wv: int = 0) -> None:
+                   top_k: int, tiles: torch.Tensor | None = None, wv: int = 0,
+                   tiles_ready: bool = False) -> None:
     """_r4d_fp8_moe_gemm_into for prefill-sized inputs: same operands and row contract, one
     workgroup per 128-row x 256-column tile of one expert (bit-identical to the decode kernel
     with sk = 1); N % 256 == 0. `tiles` is an int32 workspace of 2 * expert_ids.numel() + 1
-    entries. wq / ws_t may be pinned host tensors (read over the bus, as the cold call's full
-    tensor is)."""
+    entries; with tiles_ready it already holds moe_gemm_tiles of this align (computed once and
+    shared by the align's GEMMs) and is not rebuilt. wq / ws_t may be pinned host tensors
+    (read over the bus, as the cold call's full tensor is)."""
     K = qx.shape[1]
     N = wq.shape[1]
     nb = expert_ids.numel()
     assert y.shape == (mtk, N) and y.dtype == torch.bfloat16 and y.is_contiguous()
     assert qx.dtype == FP8 and wq.dtype == FP8 and wq.shape[2] == K
-    tiles = moe_gemm_tiles(expert_ids, num_post_pad, tiles)
+    tiles = _tile_list(expert_ids, num_post_pad, tiles, tiles_ready)
     rc = lib().rlu_moe_gemm_fp8blk_tiled(
         _p(qx), _p(x_scale), _P(device_ptr(wq)), _P(device_ptr(ws_t)), _p(sorted_ids),
         _p(expert_ids), _p(tiles),
@@ -288,18 +298,19 @@ def moe_gemm_tiled_silu_quant(q2: torch.Tensor, s2: torch.Tensor, qx: torch.Tens
                               x_scale: torch.Tensor, wq: torch.Tensor, ws_t: torch.Tensor,
                               sorted_ids: torch.Tensor, expert_ids: torch.Tensor,
                               num_post_pad: torch.Tensor, mtk: int, top_k: int,
-                              tiles: torch.Tensor | None = None) -> None:
+                              tiles: torch.Tensor | None = None,
+                              tiles_ready: bool = False) -> None:
     """moe_gemm_tiled of gate_up followed by silu_mul_quant (group 128) in one kernel: q2
     [mtk, N/2] e4m3 and s2 [mtk, N/256] f32 equal silu_mul_quant(moe_gemm_tiled(...)) bit for
     bit, rows the align does not name untouched. Raises for shapes without a kernel
-    (moe_gemm_tiled_silu_quant_built)."""
+    (moe_gemm_tiled_silu_quant_built). tiles / tiles_ready as for moe_gemm_tiled."""
     K = qx.shape[1]
     N = wq.shape[1]
     nb = expert_ids.numel()
     assert q2.shape == (mtk, N // 2) and q2.dtype == FP8 and q2.is_contiguous()
     assert s2.shape == (mtk, N // 256) and s2.dtype == torch.float32 and s2.is_contiguous()
     assert qx.dtype == FP8 and wq.dtype == FP8 and wq.shape[2] == K
-    tiles = moe_gemm_tiles(expert_ids, num_post_pad, tiles)
+    tiles = _tile_list(expert_ids, num_post_pad, tiles, tiles_ready)
     rc = lib().rlu_moe_gemm_fp8blk_tiled_silu_quant(
         _p(qx), _p(x_scale), _P(device_ptr(wq)), _P(device_ptr(ws_t)), _p(sorted_ids),
         _p(expert_ids), _p(tiles), _P(tiles.data_ptr() + 8 * nb), nb, _p(q2), _p(s2), mtk,

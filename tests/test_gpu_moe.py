@@ -663,7 +663,10 @@ def test_moe_gemm_tiled_equals_decode_kernel(ops, layer, M, wv):
     zt = torch.full((mtk, H), float("nan"), dtype=torch.bfloat16, device=DEV)
     zd = torch.full_like(zt, float("nan"))
     gpu_case(f"tiled gemm2 M={M} wv={wv}")
-    ops.moe_gemm_tiled(zt, q2_t, s2_t, layer["w2t"], layer["w2s"], *al, tw, mtk, 1, wv=wv)
+    # the align's tile list built once and handed over ready, as the layer shares it
+    tiles = ops.moe_gemm_tiles(al[1], al[2])
+    ops.moe_gemm_tiled(zt, q2_t, s2_t, layer["w2t"], layer["w2s"], *al, tw, mtk, 1, wv=wv,
+                       tiles=tiles, tiles_ready=True)
     run_gemm(ops, zd, q2_t, s2_t, layer["w2t"], layer["w2s"], al, tw, mtk, 1, npw=2, sk=1)
     torch.cuda.synchronize()
     assert not torch.isnan(zt).any()
