@@ -22,7 +22,9 @@ routed expert is read over PCIe by the GEMMs, every step) is `e2e_static_arm_ms_
 experts left cold, from the device state after each step) on this trace and on routing drawn
 from the reference's hot profile (`profile_trace`: tests/golden/hot_profile.json).
 `step_frac` is the grouped GEMMs' algorithmic bytes of a step over `ms_per_step`, as a fraction
-of 8 TB/s. `prefill_4096` times the prefill kernels on a 4096-token chunk; `cpu_baseline` the
+of 8 TB/s. `lru_fused_us_per_layer` is the fused LRU kernel (manager + both aligns) alone, the
+52 layers' calls replayed as one graph (`lru_fused_eager_us_per_layer`: the same calls
+launched eagerly). `prefill_4096` times the prefill kernels on a 4096-token chunk; `cpu_baseline` the
 layer step in torch fp32 on the host cores.
 
     python bench.py [--steps K] [--warmup W] [--only-b4]
@@ -243,7 +245,10 @@ def gemm_roofline(torch, pkg, layers, ids_last, rows, reps=3):
 
 
 def lru_us_per_layer(torch, layers, ids_dev, ids_static, t, reps=5):
-    """The fused LRU kernel alone for all 52 layers (state restored afterwards)."""
+    """The fused LRU kernel alone for all 52 layers, each call from the same state (restored
+    between repetitions, outside the timed region): (eager launches, one graph replay of the
+    52 launches) in µs per layer. The graph figure is the one comparable with the reference's
+    in-graph manager timing."""
     snap = snapshot(torch, layers)
     ids_static.copy_(ids_dev[t])
     def go():
@@ -251,17 +256,25 @@ def lru_us_per_layer(torch, layers, ids_dev, ids_static, t, reps=5):
             L.cache.fused(ids_static[l], out=L.align)
     go()
     torch.cuda.synchronize()
-    best = 1e30
-    for _ in range(reps):
-        restore(layers, snap)
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        go()
-        b.record()
-        torch.cuda.synchronize()
-        best = min(best, a.elapsed_time(b) * 1e3 / len(layers))
     restore(layers, snap)
-    return best
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        go()
+    torch.cuda.synchronize()
+    best = {"eager": 1e30, "graph": 1e30}
+    for _ in range(reps):
+        for kind, fn in (("eager", go), ("graph", g.replay)):
+            restore(layers, snap)
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            torch.cuda.synchronize()
+            best[kind] = min(best[kind], a.elapsed_time(b) * 1e3 / len(layers))
+    restore(layers, snap)
+    del g
+    return best["eager"], best["graph"]
 
 
 def lm_head_fp8(torch, pkg, dev, M=5, reps=20):
@@ -891,7 +904,7 @@ def main():
     t += args.steps
     log(f"B=4 HBM-resident step: {ms4:.3f} ms")
     roof = gemm_roofline(torch, pkg, layers4, ids4[t - 1], rows4)
-    lru_us = lru_us_per_layer(torch, layers4, ids4_dev, ids4_static, t)
+    lru_us, lru_graph_us = lru_us_per_layer(torch, layers4, ids4_dev, ids4_static, t)
     # the whole step against the grouped GEMMs' algorithmic bytes (every distinct expert once
     # per GEMM): what fraction of HBM peak the step as a whole moves
     step_bytes = roof["algorithmic_bytes_per_launch"] * 2 * LAYERS
@@ -912,7 +925,8 @@ def main():
            "roofline": roof,
            "step_frac": round(step_bytes / (ms4 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
            "step_gemm_bytes": int(step_bytes),
-           "lru_fused_us_per_layer": round(lru_us, 2),
+           "lru_fused_us_per_layer": round(lru_graph_us, 2),
+           "lru_fused_eager_us_per_layer": round(lru_us, 2),
            "wall_s_timed": round(wall4, 3)}
     if not args.only_b4:
         # the gather overlapped with the resident rows' GEMMs (the default), then the same
