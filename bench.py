@@ -396,13 +396,17 @@ def prefill_gemm(torch, pkg, dev, T=4096, reps=3, lru=True, wv=0):
 
     def timed(fn):
         # each timed call starts from an idle GPU: these kernels draw enough power that a few
-        # ms of them back to back lower the clocks, which spreads repeated timings by 10-20%
+        # ms of them back to back lower the clocks, which spreads repeated timings by 10-20%.
+        # A short spin kernel ahead of the start event keeps the GPU busy while the host
+        # enqueues the timed launches, so the events bracket GPU work only (not the Python
+        # call's own latency)
         fn()
         torch.cuda.synchronize()
         best = 1e30
         for _ in range(reps):
             time.sleep(0.1)
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda._sleep(200_000)
             a.record()
             fn()
             b.record()
