@@ -600,6 +600,56 @@ def pcie_per_step(torch, layers, g, ids_dev, ids_static, t0, k):
             round(float(np.mean(cold)), 2))
 
 
+def pcie_drift(torch, pkg, dev, rows=20, steps=400, window=50):
+    """Host-link traffic as the routing drifts: the 52 layers' caches alone (no GEMMs; the
+    fused LRU kernel decides inserts and cold experts exactly as in the layer step), LRU and
+    static arms from the same warm start, over `steps` steps of the layer traces (Zipf(1.1),
+    26 of the 512 permutation positions re-shuffled every 8 steps). Bytes per step as in
+    pcie_per_step, averaged over the first and the last `window` steps.
+    -> {arm: {"mb_first", "mb_last", "cold_first", "cold_last", "ins_first", "ins_last"}}."""
+    trace = pkg.traces
+    ids = np.empty((steps, LAYERS, rows * TOPK), np.int32)
+    warm = []
+    for l in range(LAYERS):
+        tr, perm0 = layer_trace(l, rows, steps)
+        ids[:, l] = tr.reshape(steps, rows * TOPK)
+        warm.append(trace.warm_hot(perm0, S))
+    ids_dev = torch.from_numpy(ids).to(dev)
+    out = {}
+    for arm, mi in (("lru", None), ("static", 0)):
+        caches = []
+        for hot, rank in warm:
+            c = (pkg.LruCache.build(E, hot, rank, dev) if mi is None else
+                 pkg.LruCache.build(E, hot, rank, dev, max_inserts=mi))
+            caches.append((c, c.alloc_align(rows * TOPK)))
+        seen = torch.zeros(LAYERS, E, dtype=torch.int32, device=dev)
+        ins, cold = [], []
+        for t in range(steps):
+            seen.zero_()
+            n_in = []
+            for l, (c, al) in enumerate(caches):
+                il = ids_dev[t, l].long()
+                c.fused(ids_dev[t, l], out=al)
+                n_in.append(c.n_miss[0])
+                # distinct routed experts left cold after this step's manager
+                seen[l].index_fill_(0, il[c.map_cold[il] >= 0], 1)
+            ins.append(float(torch.stack(n_in).sum().item()) / LAYERS)
+            cold.append(float(seen.sum().item()) / LAYERS)
+        mb = [(a + b) * LAYERS * EXPERT_BYTES / 1e6 for a, b in zip(ins, cold)]
+        first, last = slice(0, window), slice(steps - window, steps)
+        out[arm] = {"mb_first": round(float(np.mean(mb[first])), 1),
+                    "mb_last": round(float(np.mean(mb[last])), 1),
+                    "ins_first": round(float(np.mean(ins[first])), 2),
+                    "ins_last": round(float(np.mean(ins[last])), 2),
+                    "cold_first": round(float(np.mean(cold[first])), 2),
+                    "cold_last": round(float(np.mean(cold[last])), 2)}
+        del caches
+    out["steps"], out["window"] = steps, window
+    out["routing"] = ("the headline's layer traces (seed 1000 + layer, rows correlated), "
+                      f"{steps} steps; per-layer means over the first and last {window}")
+    return out
+
+
 def profile_routing(pkg, rows, steps):
     """Routing that follows the reference's hot profile (tests/golden/hot_profile.json: 48 MoE
     layers of routing counts from real decode and prefill traffic): layer l of the 52 draws
@@ -1070,6 +1120,11 @@ def main():
         out["pcie_mb_per_step"]["steps_counted"] = PCIE_STEPS
         del pool
         torch.cuda.empty_cache()
+        out["pcie_drift"] = pcie_drift(torch, pkg, dev)
+        log(f"drift: LRU {out['pcie_drift']['lru']['mb_first']} -> "
+            f"{out['pcie_drift']['lru']['mb_last']} MB/step, static "
+            f"{out['pcie_drift']['static']['mb_first']} -> "
+            f"{out['pcie_drift']['static']['mb_last']}")
         out["lm_head_fp8"] = lm_head_fp8(torch, pkg, dev)
         log(f"fp8 lm_head M=5: {out['lm_head_fp8']['us']} us")
         out["lm_head_w4"] = lm_head_w4(torch, pkg, dev)
