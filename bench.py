@@ -20,7 +20,8 @@ static hot/cold arm (inserts disabled: the warm-start set stays resident and eve
 routed expert is read over PCIe by the GEMMs, every step) is `e2e_static_arm_ms_per_step`.
 `pcie_mb_per_step` counts the host-link bytes of both arms (experts inserted + distinct routed
 experts left cold, from the device state after each step) on this trace and on routing drawn
-from the reference's hot profile (`profile_trace`: tests/golden/hot_profile.json).
+from the reference's hot profile (`profile_trace`: tests/golden/hot_profile.json);
+`pcie_drift` counts them over 400 steps of the drifting Zipf traces (the caches alone).
 `step_frac` is the grouped GEMMs' algorithmic bytes of a step over `ms_per_step`, as a fraction
 of 8 TB/s. `lru_fused_us_per_layer` is the fused LRU kernel (manager + both aligns) alone, the
 52 layers' calls replayed as one graph (`lru_fused_eager_us_per_layer`: the same calls
