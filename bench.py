@@ -179,26 +179,35 @@ def distinct_per_layer(ids_step):
     return np.array([len(np.unique(ids_step[l])) for l in range(ids_step.shape[0])])
 
 
-def algorithmic_bytes(ids_last, rows):
+def algorithmic_bytes(ids_last, rows, fused=False):
     """Bytes one grouped-GEMM launch must move, averaged over the 104 launches of a step: every
     distinct expert's weights and block scales once, the activations and their scales once,
-    the output rows once (and the routed weights for the down projection)."""
+    the output rows once (and the routed weights for the down projection). fused: gate_up
+    writes the bf16 activation [mtk, I] and down reads it (in place of gate_up's [mtk, 2I]
+    output and the e4m3 q2 with its scales)."""
     mtk = rows * TOPK
     total = 0.0
     d = distinct_per_layer(ids_last)
     for l in range(len(d)):
         e = int(d[l])
         total += (e * (2 * I * H + (2 * I // 128) * (H // 128) * 4)
-                  + rows * H + rows * (H // 128) * 4 + mtk * 2 * I * 2)        # gate_up
+                  + rows * H + rows * (H // 128) * 4
+                  + (mtk * I * 2 if fused else mtk * 2 * I * 2))                 # gate_up
         total += (e * (H * I + (H // 128) * (I // 128) * 4)
-                  + mtk * I + mtk * (I // 128) * 4 + mtk * H * 2 + mtk * 4)     # down
+                  + (mtk * I * 2 if fused else mtk * I + mtk * (I // 128) * 4)
+                  + mtk * H * 2 + mtk * 4)                                      # down
     return total / (2 * len(d)), d
 
 
 def gemm_launches(layers):
-    """Both grouped GEMMs of every layer, eager, on the current stream (inputs as the last step
-    left them)."""
+    """Both grouped GEMMs of every layer as the layer step runs them (gate_up with its
+    activation and down from it, or the plain pair), eager, on the current stream (inputs as
+    the last step left them)."""
     for L in layers:
+        if L.fuse_dec:
+            L._gate_up_act()
+            L._down(L.tw)
+            continue
         L._gemm_split(L.ic1, L.qx, L.xs, L.slots.w13, L.slots.s13, 0, None, L.top_k, L.npw1,
                       L.sk1)
         L._gemm_split(L.ic3, L.q2, L.s2, L.slots.w2, L.slots.s2, 2, L.tw, 1, L.npw2, L.sk2)
@@ -218,7 +227,8 @@ def gemm_roofline(torch, pkg, layers, ids_last, rows, reps=3):
     """Average duration of the grouped GEMM launches of one step (both GEMMs of all 52 layers,
     eager, back to back on the current stream, HIP events around them) and the algorithmic
     bytes each launch moves."""
-    per_launch_bytes, d = algorithmic_bytes(ids_last, rows)
+    fused = layers[0].fuse_dec
+    per_launch_bytes, d = algorithmic_bytes(ids_last, rows, fused)
     n = 2 * len(layers)
 
     def launches():
@@ -239,8 +249,11 @@ def gemm_roofline(torch, pkg, layers, ids_last, rows, reps=3):
                 frac=round(gbs / HBM_PEAK_GBS, 4),
                 traffic=None if tr is None else tr["hbm_bytes_per_launch"],
                 traffic_source=None if tr is None else tr["source"],
-                kernel=f"rlu::moe_gemm_k (gate_up npw {layers[0].npw1} sk {layers[0].sk1}, down "
-                       f"npw {layers[0].npw2} sk {layers[0].sk2}; hot + cold in one launch)",
+                kernel=(f"rlu::moe_gemm_k (gate_up npw {layers[0].npw1} sk {layers[0].sk1}"
+                        + (" with the SiLU-mul epilogue" if fused else "")
+                        + f", down npw {layers[0].npw2} sk {layers[0].sk2}"
+                        + (" quantizing the activation per workgroup" if fused else "")
+                        + "; hot + cold in one launch)"),
                 avg_launch_us=round(best, 2), algorithmic_bytes_per_launch=int(per_launch_bytes),
                 distinct_experts_per_layer=round(float(d.mean()), 1))
 
@@ -942,7 +955,7 @@ def main():
         torch.cuda.synchronize()
         c.copy_(a)
         torch.cuda.synchronize()
-        per, d = algorithmic_bytes(ids4[0], rows4)
+        per, d = algorithmic_bytes(ids4[0], rows4, layers4[0].fuse_dec)
         print(json.dumps({"pmc_probe": "52 eager layer steps, then 104 grouped-GEMM launches, "
                                        "then one 256 MiB device-to-device copy (last copy "
                                        "kernel of the run)",

@@ -148,6 +148,33 @@ int rlu_moe_gemm_split(const void* qx, const float* xs, const void* wq_hot, cons
                        void* y, int em, int mtk, int top_k, int K, int N, int wv, int sk,
                        int npw, hipStream_t stream);
 
+/* No counterpart in the reference, which runs gate_up into ic1 [mtk, N] and then
+ * fused_silu_mul_quant (r4d_mxfp4_moe.py.lru.diff:659-696, kernels/fused_silu_mul_quant.py:
+ * 26-101): rlu_moe_gemm_split of gate_up (npw 2) with the SiLU-mul in its epilogue. act bf16
+ * [mtk, N/2] = bf16(silu(g) x u) of the GEMM's bf16 outputs g (columns [0, N/2)) and u
+ * ([N/2, N)), the activation rlu_silu_mul_quant computes from rlu_moe_gemm_split's y, bit for
+ * bit, on every row the aligns name (other rows untouched). wq == NULL runs the hot list alone.
+ * N % 256 == 0; other checks and codes as rlu_moe_gemm_split (no topk_weights, no npw). */
+int rlu_moe_gemm_split_act(const void* qx, const float* xs, const void* wq_hot,
+                           const float* ws_hot, const int* sorted_hot, const int* eids_hot,
+                           const int* npad_hot, const void* wq, const float* ws,
+                           const int* sorted_cold, const int* eids_cold, const int* npad_cold,
+                           void* act, int em, int mtk, int top_k, int K, int N, int wv, int sk,
+                           hipStream_t stream);
+
+/* No counterpart in the reference (see rlu_moe_gemm_split_act): the down projection of the split
+ * GEMM reading the bf16 activation act [mtk, K] instead of q2 / s2. Each workgroup quantizes
+ * the rows of its block per 128-column group exactly as rlu_silu_mul_quant (group 128) does,
+ * so y equals rlu_moe_gemm_split (npw 4, sk 1, top_k 1) on that kernel's q2 / s2, bit for bit,
+ * with topk_weights as there. wq == NULL runs the hot list alone. K % 128 == 0, K <= 1024,
+ * N % 256 == 0; -1 / -2 on bad sizes or null operands. */
+int rlu_moe_gemm_split_qin(const void* act, const void* wq_hot, const float* ws_hot,
+                           const int* sorted_hot, const int* eids_hot, const int* npad_hot,
+                           const void* wq, const float* ws, const int* sorted_cold,
+                           const int* eids_cold, const int* npad_cold,
+                           const float* topk_weights, void* y, int em, int mtk, int K, int N,
+                           hipStream_t stream);
+
 /* Replaces fp8hip_gemm_w8a8_launch behind gemm_fp8_block (kernels/fp8_target_lmhead.py:70-74):
  * y [M, N] bf16 = qx [M, K] (xs [M, K/128]) x w [N, K] (ws [N/128, K/128])^T, 1 <= M <= 16,
  * w in fragment order (rlu_shuffle_fp8_weight), as fp8hip takes shuffle_weight_gfx1201 output. */

@@ -32,6 +32,8 @@ SIGNATURES: dict[str, tuple] = {
     "r4d_gemm_moe_fp8blk_nt_b16": (_I, [_P] * 10 + [_I] * 8 + [_P]),
     "rlu_gemm_fp8blk_m16": (_I, [_P] * 5 + [_I] * 5 + [_P]),
     "rlu_moe_gemm_split": (_I, [_P] * 14 + [_I] * 8 + [_P]),
+    "rlu_moe_gemm_split_act": (_I, [_P] * 13 + [_I] * 7 + [_P]),
+    "rlu_moe_gemm_split_qin": (_I, [_P] * 13 + [_I] * 4 + [_P]),
     "rlu_shuffle_fp8_weight": (_I, [_P, _P, _LL, _I, _P]),
     "rlu_gemm_w4_m16": (_I, [_P, _I, _I, _P, _P, _P, _I, _I, _P]),
     "rlu_pack_w4": (_I, [_P, _I, _LL, _I, _I, _I, _P, _P, _P]),

@@ -29,31 +29,50 @@
 #include "gemm_common.h"
 #include "gemm_item.h"
 #include "numerics.h"
+#include "quant_row.h"
 #include "rlu.h"
 #include "wave.h"
 
 namespace rlu {
 
 constexpr int GWV = 4;      // waves per workgroup
+constexpr int QIN_MAXG = 8;   // 128-column groups of the activation MODE 2 reads (K <= 1024)
+constexpr int QIN_G = 4;      // waves per workgroup in MODE 2 (items of one block): with 8,
+                              // 40 column tiles x 48 blocks leave CUs idle at B=4 (3.68 ms
+                              // per 52-layer step against 3.57)
 
-template <int NPW, int SKW, bool DENSE>
-__global__ __launch_bounds__(GWV * WAVE) void moe_gemm_k(
+// MODE 0: y [mtk, N] = the GEMM (routed weights optional).
+// MODE 1 (gate_up with its activation, NPW / 2 gate + NPW / 2 up strips per item): y
+// [mtk, N / 2] = bf16(silu(g) x u) of the GEMM's bf16 outputs g (column c) and u (column
+// N / 2 + c), computed as silu_mul_quant_k computes them from the [mtk, N] output.
+// MODE 2 (down from the activation, SKW = 1, the G items of a workgroup in one block): qx is
+// the bf16 activation [mtk, K] and xs is not read; the workgroup first quantizes its block's 16
+// rows per 128-column group exactly as silu_mul_quant_k does (same amax, scale and rounding)
+// into LDS, which the MFMAs then read, so the output equals MODE 0 on that kernel's q2 / s2.
+template <int NPW, int SKW, bool DENSE, int MODE = 0, int G = GWV>
+__global__ __launch_bounds__(G * WAVE) void moe_gemm_k(
     const uint8_t* __restrict__ qx, const float* __restrict__ xs, WSet s0, WSet s1, int nsets,
     uint16_t* __restrict__ y, const float* __restrict__ tw, int mtk, int top_k, int K, int N) {
-  constexpr int IPG = GWV / SKW;                    // items per workgroup pass
-  extern __shared__ float lds[];                    // [GWV][nsteps][16] scales, then partials
+  constexpr bool PAIR = MODE == 1, AL = MODE == 2;
+  constexpr int NH = PAIR ? 2 : 1;                  // weight-scale rows per item
+  constexpr int IPG = G / SKW;                      // items per workgroup pass
+  extern __shared__ float lds[];                    // [G][nsteps][NH][16] scales, then
+                                                    // partials (SKW > 1) or the A rows (AL)
   const int lane = lane_id();
   const int wv = uniform(threadIdx.x / WAVE);       // wave-uniform: item metadata in SGPRs
   const int sub = wv / SKW, ks = wv % SKW;
   const int nsteps = item_steps<NPW, SKW>(K);
-  const int NT = 16 * NPW;
-  const int ntiles = N / NT;
+  const int NT = PAIR ? 8 * NPW : 16 * NPW;         // output columns per item
+  const int ntiles = (PAIR ? N / 2 : N) / NT;
   const int nb0 = DENSE ? 1 : (s0.npad[0] >> 4);
   const int nb1 = (DENSE || nsets < 2) ? 0 : (s1.npad[0] >> 4);
   const int nitems = (nb0 + nb1) * ntiles;
   const int ngroups = (nitems + IPG - 1) / IPG;
-  float* sx = lds + (size_t)wv * nsteps * 16;
-  float* red = lds + (size_t)GWV * nsteps * 16;     // [2][GWV][NPW * 4][64]
+  float* sx = lds + (size_t)wv * nsteps * 16 * NH;
+  float* red = lds + (size_t)G * nsteps * 16 * NH;  // [2][G][NPW * 4][64]
+  const int als = K + 16;                           // AL: LDS row stride of the A rows
+  uint8_t* alds = reinterpret_cast<uint8_t*>(red);  // AL: [16][als] e4m3, then [16][K/128] f32
+  float* xsl = reinterpret_cast<float*>(alds + 16 * als);
   const int r16 = lane & 15;
   int parity = 0;
 
@@ -95,24 +114,86 @@ __global__ __launch_bounds__(GWV * WAVE) void moe_gemm_k(
 #pragma unroll
     for (int s = 0; s < NPW; ++s) acc[s] = v4f{0.f, 0.f, 0.f, 0.f};
     float twv[4] = {1.f, 1.f, 1.f, 1.f};
-    if (live)
-      item_mma<NPW, SKW, DENSE>(qx, xs, wq, ws, so, eid, n0, tw, mtk, top_k, K, N, ks, sx, acc,
-                                sod, twv);
+    if constexpr (AL) {
+      // MODE 2: the G items of the workgroup share block b (ntiles % G == 0, no item past
+      // nitems), so the workgroup quantizes the block's 16 rows into LDS together -- 16-lane
+      // group q takes row q % 16 and every (G / 4)-th 128-column group from q / 16 on, lane
+      // l16 columns [8 l16, 8 l16 + 8) of each -- once its item's first weight steps are in
+      // flight; then one workgroup barrier
+      constexpr int GS = G / 4;                     // 128-column group stride of a 16-lane group
+      static_assert(G % 4 == 0 && SKW == 1, "16-lane groups cover the block's 16 rows");
+      const int q16 = (int)threadIdx.x / 16, r = q16 % 16, g0 = q16 / 16;
+      const int l16 = lane & 15, ng = K / 128;
+      const int sr = sids[b * 16 + r];
+      auto pro = [&]() __attribute__((always_inline)) {
+        if (eid >= 0) {
+          const bool ok = sr < mtk;
+          const uint16_t* src =
+              reinterpret_cast<const uint16_t*>(qx) + (size_t)(ok ? sr : 0) * K + 8 * l16;
+          constexpr int NP = (QIN_MAXG + GS - 1) / GS;
+          uint4 raw[NP];
+#pragma unroll
+          for (int p = 0; p < NP; ++p)
+            if (g0 + p * GS < ng)
+              raw[p] = *reinterpret_cast<const uint4*>(src + (g0 + p * GS) * 128);
+#pragma unroll
+          for (int p = 0; p < NP; ++p) {
+            const int g = g0 + p * GS;
+            if (g < ng) {
+              float v[8];
+              unpack8_bf16(raw[p], v);
+              uint32_t m = 0;
+#pragma unroll
+              for (int j = 0; j < 8; ++j) {
+                v[j] = ok ? v[j] : 0.f;
+                m = max(m, abs_bits(v[j]));
+              }
+              const float sc = scale_of(row_max_u32(m));
+              *reinterpret_cast<uint2*>(alds + r * als + g * 128 + 8 * l16) = quant8(v, sc);
+              if (l16 == 0) xsl[r * ng + g] = sc;
+            }
+          }
+        }
+        lds_barrier();
+      };
+      if (live)
+        item_mma<NPW, SKW, DENSE, ring_of(NPW), PAIR, AL>(qx, xs, wq, ws, so, eid, n0, tw, mtk,
+                                                          top_k, K, N, ks, sx, acc, sod, twv,
+                                                          alds, als, xsl, pro);
+      else
+        pro();
+    } else if (live) {
+      item_mma<NPW, SKW, DENSE, ring_of(NPW), PAIR, AL>(qx, xs, wq, ws, so, eid, n0, tw, mtk,
+                                                        top_k, K, N, ks, sx, acc, sod, twv);
+    }
     if (SKW > 1)
-      splitk_reduce<NPW, SKW>(acc, red + (size_t)parity * GWV * NPW * 4 * WAVE, wv, ks);
+      splitk_reduce<NPW, SKW>(acc, red + (size_t)parity * G * NPW * 4 * WAVE, wv, ks);
     if (live && ks == 0) {
       // epilogue: rows this lane holds, routed weight, bf16, only live rows
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int o = sod[i];
         if (o < mtk) {
+          if constexpr (PAIR) {
 #pragma unroll
-          for (int s = 0; s < NPW; ++s)
-            y[(size_t)o * N + n0 + s * 16 + r16] = f32_to_bf16(acc[s][i] * twv[i]);
+            for (int s = 0; s < NPW / 2; ++s) {
+              const float g = bf16_to_f32(f32_to_bf16(acc[s][i] * twv[i]));
+              const float u = bf16_to_f32(f32_to_bf16(acc[s + NPW / 2][i] * twv[i]));
+              y[(size_t)o * (N / 2) + n0 + s * 16 + r16] =
+                  f32_to_bf16(__fmul_rn(silu_bf16(g), u));
+            }
+          } else {
+#pragma unroll
+            for (int s = 0; s < NPW; ++s)
+              y[(size_t)o * N + n0 + s * 16 + r16] = f32_to_bf16(acc[s][i] * twv[i]);
+          }
         }
       }
     }
-    wave_lds_sync();                                // sx is rewritten by the next item
+    if constexpr (AL)
+      lds_barrier();                                // the A rows are rewritten by the next group
+    else
+      wave_lds_sync();                              // sx is rewritten by the next item
   }
 }
 
@@ -139,18 +220,21 @@ static int pick_sk(int nkg, int sk) {
   return 1;
 }
 
-template <bool DENSE>
+// MODE 1 is built for npw 2 (any sk), MODE 2 for npw 4 with sk 1 (-6 / -4 otherwise).
+template <bool DENSE, int MODE = 0>
 int launch(int npw, int sk, int grid, hipStream_t st, const uint8_t* qx, const float* xs,
            WSet s0, WSet s1, int nsets, uint16_t* y, const float* tw, int mtk, int top_k,
            int K, int N) {
   const int kpw = K / 128 / sk;
   const int d = ring_of(npw);
   const int nsteps = (kpw + d - 1) / d * d;
-  const size_t lds =
-      ((size_t)GWV * nsteps * 16 + (sk > 1 ? 2 * (size_t)GWV * npw * 4 * WAVE : 0)) * 4;
-#define RLU_L(P, SK)                                                                            \
-  hipLaunchKernelGGL((moe_gemm_k<P, SK, DENSE>), dim3(grid), dim3(GWV * WAVE), lds, st, qx, xs, \
-                     s0, s1, nsets, y, tw, mtk, top_k, K, N)
+  constexpr int G = MODE == 2 ? QIN_G : GWV;
+  const size_t tail = MODE == 2 ? (size_t)16 * (K + 16) + (size_t)16 * (K / 128) * 4
+                                : (sk > 1 ? 2 * (size_t)G * npw * 4 * WAVE * 4 : 0);
+  const size_t lds = (size_t)G * nsteps * 16 * (MODE == 1 ? 2 : 1) * 4 + tail;
+#define RLU_L(P, SK)                                                                          \
+  hipLaunchKernelGGL((moe_gemm_k<P, SK, DENSE, MODE, G>), dim3(grid), dim3(G * WAVE), lds,    \
+                     st, qx, xs, s0, s1, nsets, y, tw, mtk, top_k, K, N)
 #define RLU_SK(P)                   \
   switch (sk) {                     \
     case 1: RLU_L(P, 1); break;     \
@@ -158,12 +242,21 @@ int launch(int npw, int sk, int grid, hipStream_t st, const uint8_t* qx, const f
     case 4: RLU_L(P, 4); break;     \
     default: return -4;             \
   }
-  switch (npw) {
-    case 1: RLU_SK(1); break;
-    case 2: RLU_SK(2); break;
-    case 4: RLU_SK(4); break;
-    case 8: RLU_SK(8); break;
-    default: return -6;
+  if constexpr (MODE == 1) {
+    if (npw != 2) return -6;
+    RLU_SK(2);
+  } else if constexpr (MODE == 2) {
+    if (npw != 4) return -6;
+    if (sk != 1) return -4;
+    RLU_L(4, 1);
+  } else {
+    switch (npw) {
+      case 1: RLU_SK(1); break;
+      case 2: RLU_SK(2); break;
+      case 4: RLU_SK(4); break;
+      case 8: RLU_SK(8); break;
+      default: return -6;
+    }
   }
 #undef RLU_SK
 #undef RLU_L
@@ -246,6 +339,65 @@ int rlu_moe_gemm_split(const void* qx, const float* xs, const void* wq_hot, cons
   const rlu::WSet s1{(const uint8_t*)wq, ws, sorted_cold, eids_cold, npad_cold};
   return rlu::launch<false>(npw, sk, grid, stream, (const uint8_t*)qx, xs, s0, s1, 2,
                             (uint16_t*)y, topk_weights, mtk, top_k, K, N);
+}
+
+// gate_up of the split GEMM with SiLU-mul in its epilogue: act [mtk, N / 2] bf16 =
+// bf16(silu(g) x u) of the GEMM's bf16 outputs g = columns [0, N / 2), u = [N / 2, N), the
+// activation silu_mul_quant computes from rlu_moe_gemm_split's output, bit for bit, on the
+// rows the aligns name (no [mtk, N] intermediate, and no activation launch). wq == NULL runs
+// the hot list alone. npw is 2 (two strips: a gate column block and its up block); N % 256.
+int rlu_moe_gemm_split_act(const void* qx, const float* xs, const void* wq_hot,
+                           const float* ws_hot, const int* sorted_hot, const int* eids_hot,
+                           const int* npad_hot, const void* wq, const float* ws,
+                           const int* sorted_cold, const int* eids_cold, const int* npad_cold,
+                           void* act, int em, int mtk, int top_k, int K, int N, int wv, int sk,
+                           hipStream_t stream) {
+  if (em < 1 || mtk < 0 || top_k < 1 || K <= 0 || N <= 0) return -1;
+  if (!qx || !xs || !wq_hot || !ws_hot || !sorted_hot || !eids_hot || !npad_hot || !act)
+    return -1;
+  const int nsets = wq ? 2 : 1;
+  if (nsets == 2 && (!ws || !sorted_cold || !eids_cold || !npad_cold)) return -1;
+  if (K % 128 || N % 256) return -2;
+  sk = rlu::pick_sk(K / 128, sk);
+  if (rlu::bad_sk(K, sk)) return -4;
+  if (wv < 0 || wv > 16) return -5;
+  if (mtk == 0) return 0;
+  const int nb = (em + 15) / 16;
+  const int nblive = nsets * nb < mtk ? nsets * nb : mtk;
+  const int items = nblive * (N / 32);
+  const int grid = rlu::grid_for(items, sk, wv);
+  const rlu::WSet s0{(const uint8_t*)wq_hot, ws_hot, sorted_hot, eids_hot, npad_hot};
+  const rlu::WSet s1{(const uint8_t*)wq, ws, sorted_cold, eids_cold, npad_cold};
+  return rlu::launch<false, 1>(2, sk, grid, stream, (const uint8_t*)qx, xs, s0, nsets == 2 ? s1 : s0,
+                               nsets, (uint16_t*)act, nullptr, mtk, top_k, K, N);
+}
+
+// down of the split GEMM from the bf16 activation act [mtk, K] (rlu_moe_gemm_split_act's
+// output): each workgroup quantizes its block's rows per 128-column group as silu_mul_quant
+// does (same scales and codes) and runs the down GEMM on them, so y equals
+// rlu_moe_gemm_split (npw 4, sk 1) on silu_mul_quant's q2 / s2, bit for bit. Routed weights
+// as there; wq == NULL runs the hot list alone. K <= 1024, N % 256 == 0.
+int rlu_moe_gemm_split_qin(const void* act, const void* wq_hot, const float* ws_hot,
+                           const int* sorted_hot, const int* eids_hot, const int* npad_hot,
+                           const void* wq, const float* ws, const int* sorted_cold,
+                           const int* eids_cold, const int* npad_cold,
+                           const float* topk_weights, void* y, int em, int mtk, int K, int N,
+                           hipStream_t stream) {
+  if (em < 1 || mtk < 0 || K <= 0 || N <= 0) return -1;
+  if (!act || !wq_hot || !ws_hot || !sorted_hot || !eids_hot || !npad_hot || !y) return -1;
+  const int nsets = wq ? 2 : 1;
+  if (nsets == 2 && (!ws || !sorted_cold || !eids_cold || !npad_cold)) return -1;
+  if (K % 128 || N % (64 * rlu::QIN_G) || K > 128 * rlu::QIN_MAXG) return -2;
+  if (mtk == 0) return 0;
+  const int nb = (em + 15) / 16;
+  const int nblive = nsets * nb < mtk ? nsets * nb : mtk;
+  const int items = nblive * (N / 64);
+  const int grid = (items + rlu::QIN_G - 1) / rlu::QIN_G;
+  const rlu::WSet s0{(const uint8_t*)wq_hot, ws_hot, sorted_hot, eids_hot, npad_hot};
+  const rlu::WSet s1{(const uint8_t*)wq, ws, sorted_cold, eids_cold, npad_cold};
+  return rlu::launch<false, 2>(4, 1, grid, stream, (const uint8_t*)act, nullptr, s0,
+                               nsets == 2 ? s1 : s0, nsets, (uint16_t*)y, topk_weights, mtk, 1,
+                               K, N);
 }
 
 // Dense fp8 block-scaled GEMM for M <= 16 (the target lm_head): y[M, N] bf16 <- qx[M, K] e4m3

@@ -34,8 +34,19 @@ __host__ __device__ __forceinline__ int item_steps(int K) {
 // (sod; mtk = padding) and, for wave ks == 0 when tw is given, their routed weights (twv).
 // so / sod: this lane's A row and its four output rows, which the caller takes from the
 // block's 16 sorted ids, loaded together with the expert id.
-// sx: this wave's item_steps() x 16 floats of LDS. D: register ring depth.
-template <int NPW, int SKW, bool DENSE, int D = ring_of(NPW)>
+// sx: this wave's item_steps() x 16 floats of LDS (x 2 with PAIR). D: register ring depth.
+// PAIR (gate_up with its activation): the first NPW / 2 strips are gate columns n0 + 16 s,
+// the others the matching up columns N / 2 + n0 + 16 (s - NPW / 2), each half with its own
+// weight-block scales, so a lane holds gate and up of the same (row, column).
+// AL: the A operand is the block's 16 rows in LDS (alds: row r at r * als bytes, xsl: their
+// K / 128 scales per row), for SKW = 1; qx / xs are not read. pro() runs once the first D
+// weight steps are in flight and before anything reads LDS: with AL it fills alds / xsl.
+struct NoPro {
+  __device__ void operator()() const {}
+};
+
+template <int NPW, int SKW, bool DENSE, int D = ring_of(NPW), bool PAIR = false, bool AL = false,
+          class PRO = NoPro>
 __device__ __forceinline__ void item_mma(const uint8_t* __restrict__ qx,
                                          const float* __restrict__ xs,
                                          const uint8_t* __restrict__ wq,
@@ -43,7 +54,13 @@ __device__ __forceinline__ void item_mma(const uint8_t* __restrict__ qx,
                                          int so, int eid, int n0,
                                          const float* __restrict__ tw, int mtk, int top_k, int K,
                                          int N, int ks, float* sx, v4f (&acc)[NPW],
-                                         int (&sod)[4], float (&twv)[4]) {
+                                         int (&sod)[4], float (&twv)[4],
+                                         const uint8_t* alds = nullptr, int als = 0,
+                                         const float* xsl = nullptr, const PRO& pro = PRO()) {
+  static_assert(!PAIR || (NPW % 2 == 0 && !DENSE), "gate / up pairs");
+  static_assert(!AL || (SKW == 1 && !DENSE), "A from LDS: one wave per item");
+  constexpr int NH = PAIR ? 2 : 1;                  // weight-scale rows per item
+  constexpr int HALF = NPW / 2 > 0 ? NPW / 2 : 1;   // strips per half with PAIR
   const int lane = lane_id();
   const int r16 = lane & 15, c4 = lane >> 4;
   const int nkg = K / 128;
@@ -56,49 +73,75 @@ __device__ __forceinline__ void item_mma(const uint8_t* __restrict__ qx,
   const bool valid = so < mtk;
   const int arow = valid ? so / top_k : 0;
   const int kg0 = ks * kpw;
-  // activation scale x weight-block scale for step k = 4 m + c4 of row r16; issued before the
-  // weight loads so that staging them waits for nothing else
-  const float* xrow = xs + (size_t)arow * nkg + kg0;
-  const float* wsr = ws + ((size_t)eid * (N / 128) + n0 / 128) * nkg + kg0;
-  float xv[XM], wv_[XM];
+  // activation scale x weight-block scale for step k = 4 m + c4 of row r16 (per half with
+  // PAIR); issued before the weight loads so that staging them waits for nothing else
+  const float* xrow = AL ? xsl + (size_t)r16 * nkg : xs + (size_t)arow * nkg + kg0;
+  // strip s's first column and its offset from strip 0 in the fragment-order weights
+  auto scol = [&](int s) __attribute__((always_inline)) {
+    return PAIR ? (s < NPW / 2 ? n0 + 16 * s : N / 2 + n0 + 16 * (s - NPW / 2)) : n0 + 16 * s;
+  };
+  const float* wsr[NH];
+#pragma unroll
+  for (int h = 0; h < NH; ++h)
+    wsr[h] = ws + ((size_t)eid * (N / 128) + scol(h * HALF) / 128) * nkg + kg0;
+  float xv[XM], wv_[NH][XM];
 #pragma unroll
   for (int m = 0; m < XM; ++m) {
     if (4 * m < nsteps) {                           // uniform; the product waits for the store
       const int k = min(4 * m + c4, kpw - 1);
-      xv[m] = xrow[k];
-      wv_[m] = wsr[k];
+      if (!AL) xv[m] = xrow[k];
+#pragma unroll
+      for (int h = 0; h < NH; ++h) wv_[h][m] = wsr[h][k];
     }
   }
-  const uint8_t* A = qx + (size_t)arow * K + kg0 * 128 + 16 * c4;
+  const uint8_t* A = AL ? alds + (size_t)r16 * als + 16 * c4
+                        : qx + (size_t)arow * K + kg0 * 128 + 16 * c4;
   const uint8_t* W = wq + ((size_t)eid * N + n0) * K + (size_t)kg0 * 2048 + lane * 16;
   v4u ra[D][2], rb[D][NPW][2];
   auto issue = [&](int j, int k) {
-    ra[j][0] = *reinterpret_cast<const v4u*>(A + k * 128);
-    ra[j][1] = *reinterpret_cast<const v4u*>(A + k * 128 + 64);
+    if (!AL) {
+      ra[j][0] = *reinterpret_cast<const v4u*>(A + k * 128);
+      ra[j][1] = *reinterpret_cast<const v4u*>(A + k * 128 + 64);
+    }
 #pragma unroll
     for (int s = 0; s < NPW; ++s) {
-      const v4u* p = reinterpret_cast<const v4u*>(W + (size_t)s * 16 * K + (size_t)k * 2048);
+      const v4u* p = reinterpret_cast<const v4u*>(W + (size_t)(scol(s) - n0) * K +
+                                                  (size_t)k * 2048);
       rb[j][s][0] = __builtin_nontemporal_load(p);
       rb[j][s][1] = __builtin_nontemporal_load(p + 64);
     }
   };
   auto step = [&](int j, int k) {
-    const v4f f = *reinterpret_cast<const v4f*>(sx + k * 16 + 4 * c4);
-    const v8i av = pack8(ra[j][0], ra[j][1]);
+    v4f f[NH];
+#pragma unroll
+    for (int h = 0; h < NH; ++h)
+      f[h] = *reinterpret_cast<const v4f*>(sx + (k * NH + h) * 16 + 4 * c4);
+    const v8i av = AL ? pack8(*reinterpret_cast<const v4u*>(A + k * 128),
+                              *reinterpret_cast<const v4u*>(A + k * 128 + 64))
+                      : pack8(ra[j][0], ra[j][1]);
 #pragma unroll
     for (int s = 0; s < NPW; ++s) {
       const v4f d = mfma_f8(av, pack8(rb[j][s][0], rb[j][s][1]));
+      const int h = PAIR ? s / HALF : 0;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[s][i] = fmaf(d[i], f[i], acc[s][i]);
+      for (int i = 0; i < 4; ++i) acc[s][i] = fmaf(d[i], f[h][i], acc[s][i]);
     }
   };
 #pragma unroll
   for (int j = 0; j < D; ++j) issue(j, min(j, kpw - 1));
+  pro();
+  if (AL) {
+#pragma unroll
+    for (int m = 0; m < XM; ++m)
+      if (4 * m < nsteps) xv[m] = xrow[min(4 * m + c4, kpw - 1)];
+  }
 #pragma unroll
   for (int m = 0; m < XM; ++m) {
     const int k = 4 * m + c4;
     if (4 * m < nsteps && k < nsteps)
-      sx[k * 16 + r16] = (k < kpw && valid) ? xv[m] * wv_[m] : 0.f;
+#pragma unroll
+      for (int h = 0; h < NH; ++h)
+        sx[(k * NH + h) * 16 + r16] = (k < kpw && valid) ? xv[m] * wv_[h][m] : 0.f;
   }
   wave_lds_sync();
   int c0 = 0;

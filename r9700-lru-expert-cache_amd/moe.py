@@ -62,7 +62,8 @@ class LruMoELayer:
                  top_k: int, device="cuda", slots: ExpertWeights | None = None,
                  npw1: int = 2, npw2: int = 4, sk1: int | None = None, sk2: int = 1,
                  wv: int = 0, max_inserts: int | None = None,
-                 prefill_rows: int = PREFILL_ROWS, fold_sum: bool | None = None):
+                 prefill_rows: int = PREFILL_ROWS, fold_sum: bool | None = None,
+                 fuse_act: bool | None = None):
         """npw / sk: 16-column tiles per item and K split of gate_up (1) and down (2); the
         defaults are the fastest measured at the decode shapes (hidden 2560, intermediate
         768): gate_up splits K over 2 waves above 8 tokens (20 tokens: 3.70 vs 3.95 ms per
@@ -83,7 +84,15 @@ class LruMoELayer:
         fold_sum: run down and moe_sum as one token-major kernel (ops.moe_down_sum, the same
         output bit for bit) when the gather is not overlapped; default on up to
         FOLD_SUM_TOKENS tokens at the shapes the kernel is built for (intermediate 768,
-        top-10)."""
+        top-10).
+
+        fuse_act (decode): gate_up writes the SiLU-mul activation from its epilogue
+        (ops.moe_gemm_split_act) and down quantizes it per workgroup
+        (ops.moe_gemm_split_qin), in place of gate_up into ic1, silu_mul_quant and down on
+        q2 / s2: the same output bit for bit, one launch fewer per layer (two with the gather
+        overlap). Default on for decode layers that do not fold down and moe_sum, at npw 2 / 4,
+        sk2 = 1, wv = 0, 2 I % 256 == 0, hidden % 256 == 0 and I <= 1024; prefill layers fuse
+        the activation into their own gate_up."""
         dev = torch.device(device)
         self.full = full
         self.full_ptrs = full.ptrs()
@@ -131,7 +140,15 @@ class LruMoELayer:
         # prefill gate_up with SiLU-mul-quant in its epilogue where a kernel is built for the
         # shape: no [mtk, 2I] bf16 intermediate (same q2 / s2 bits)
         self.fuse_act = self.prefill and ops.moe_gemm_tiled_silu_quant_built(self.H, self.N1)
-        self.ic1 = (None if self.fuse_act else
+        # decode: gate_up with its activation, down quantizing it (no activation launch)
+        if fuse_act is None:
+            fuse_act = (not self.prefill and not self.fold_sum and npw1 == 2 and npw2 == 4
+                        and sk2 == 1 and wv == 0 and self.N1 % 256 == 0
+                        and self.H % 256 == 0 and self.I <= 1024)
+        self.fuse_dec = bool(fuse_act) and not self.prefill and not self.fold_sum
+        self.act = (torch.empty((self.mtk, self.I), dtype=torch.bfloat16, device=dev)
+                    if self.fuse_dec else None)
+        self.ic1 = (None if self.fuse_act or self.fuse_dec else
                     torch.empty((self.mtk, self.N1), dtype=torch.bfloat16, device=dev))
         self.q2 = torch.empty((self.mtk, self.I), dtype=ops.FP8, device=dev)
         self.s2 = torch.empty((self.mtk, self.I // 128), dtype=torch.float32, device=dev)
@@ -206,6 +223,22 @@ class LruMoELayer:
                         src_ptrs=[p for _, _, p in pairs])
 
     # -- _gemm_split: resident slots + the full tensor, one launch ----------------------------
+    def _down(self, tw, eh=None, cold=True):
+        """The down projection into ic3 over the hot align (block ids eh) and, with cold, the
+        cold align."""
+        if self.fuse_dec:
+            sh, eh0, nh, sc, ec, nc = self.align
+            ops.moe_gemm_split_qin(
+                self.ic3, self.act, self.slots.w2, self.slots.s2,
+                (sh, eh0 if eh is None else eh, nh), tw, self.mtk,
+                *((self.full.w2, self.full.s2, (sc, ec, nc)) if cold else ()))
+            return
+        down = (self.ic3, self.q2, self.s2, self.slots.w2, self.slots.s2)
+        if cold:
+            self._gemm_split(*down, 2, tw, 1, self.npw2, self.sk2, eh=eh)
+        else:
+            self._gemm_hot(*down, tw, 1, self.npw2, self.sk2, eh)
+
     def _gemm_split(self, y, qx, xs, slot_w, slot_s, part, tw, top_k, npw, sk, eh=None):
         """part: 0 gate_up, 2 down (the index of its weight buffer in ExpertWeights.tensors);
         eh replaces the hot align's block expert ids (the overlap's resident bucket)."""
@@ -257,6 +290,14 @@ class LruMoELayer:
     # -- gate_up and the activation quant over the hot align (block ids eh) and, with cold,
     # the cold align -------------------------------------------------------------------------
     def _gate_up_act(self, eh=None, cold=True):
+        if self.fuse_dec:
+            sh, eh0, nh, sc, ec, nc = self.align
+            ops.moe_gemm_split_act(
+                self.act, self.qx, self.xs, self.slots.w13, self.slots.s13,
+                (sh, eh0 if eh is None else eh, nh), self.mtk, self.top_k,
+                *((self.full.w13, self.full.s13, (sc, ec, nc)) if cold else ()), wv=self.wv,
+                sk=self.sk1)
+            return
         if self.fuse_act:
             sh, eh0, nh, sc, ec, nc = self.align
             for w, s, al in (((self.slots.w13, self.slots.s13, (sh, eh0 if eh is None else eh,
@@ -306,16 +347,15 @@ class LruMoELayer:
         if tw.dtype != torch.float32 or not tw.is_contiguous():   # as fused_topk already gives
             self.tw.copy_(tw)
             tw = self.tw
-        down = (self.ic3, self.q2, self.s2, self.slots.w2, self.slots.s2)
         if overlap:
             split_fresh(self.align[1], self.cache.miss, self.cache.n_miss, self.cache.S,
                         self.eids_res, self.eids_new)
             self._gate_up_act(eh=self.eids_res)
-            self._gemm_split(*down, 2, tw, 1, self.npw2, self.sk2, eh=self.eids_res)
+            self._down(tw, eh=self.eids_res)
             torch.cuda.current_stream().wait_event(self.ev_up)
             self._gate_up_act(eh=self.eids_new, cold=False)
             torch.cuda.current_stream().wait_stream(waited)
-            self._gemm_hot(*down, tw, 1, self.npw2, self.sk2, self.eids_new)
+            self._down(tw, eh=self.eids_new, cold=False)
         else:
             if waited is not None:
                 torch.cuda.current_stream().wait_stream(waited)
@@ -329,5 +369,5 @@ class LruMoELayer:
                                  self.cache.table, self.slots.w2, self.slots.s2, self.full.w2,
                                  self.full.s2, output)
                 return
-            self._gemm_split(*down, 2, tw, 1, self.npw2, self.sk2)
+            self._down(tw)
         ops.moe_sum(self.ic3.view(M, self.top_k, self.H), output)

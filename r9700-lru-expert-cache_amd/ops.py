@@ -146,6 +146,47 @@ def _r4d_fp8_moe_gemm(qx: torch.Tensor, x_scale: torch.Tensor, wq: torch.Tensor,
     return y
 
 
+def moe_gemm_split_act(act: torch.Tensor, qx: torch.Tensor, x_scale: torch.Tensor,
+                       w_hot: torch.Tensor, s_hot: torch.Tensor, align_hot, mtk: int, top_k: int,
+                       w_cold: torch.Tensor | None = None, s_cold: torch.Tensor | None = None,
+                       align_cold=None, wv: int = 0, sk: int = 0) -> None:
+    """gate_up of the split GEMM (npw 2) with the SiLU-mul in its epilogue: act [mtk, N/2]
+    bf16 equals silu_mul_quant's activation of the [mtk, N] gate_up output, bit for bit, on
+    every row the aligns name. align_* = (sorted_ids, expert_ids, num_post_pad); without a
+    cold set the hot list runs alone. w_cold / s_cold may be pinned host tensors."""
+    N, K = w_hot.shape[1], w_hot.shape[2]
+    assert act.shape == (mtk, N // 2) and act.dtype == torch.bfloat16 and act.is_contiguous()
+    assert qx.dtype == FP8 and w_hot.dtype == FP8 and qx.shape[1] == K
+    sh, eh, nh = align_hot
+    sc, ec, nc = align_cold if align_cold is not None else (None, None, None)
+    rc = lib().rlu_moe_gemm_split_act(
+        _p(qx), _p(x_scale), _p(w_hot), _p(s_hot), _p(sh), _p(eh), _p(nh),
+        _P(device_ptr(w_cold)) if w_cold is not None else _P(0),
+        _P(device_ptr(s_cold)) if s_cold is not None else _P(0), _p(sc), _p(ec), _p(nc),
+        _p(act), sh.numel(), mtk, top_k, K, N, wv, sk, _P(stream_ptr()))
+    check(rc, "rlu_moe_gemm_split_act")
+
+
+def moe_gemm_split_qin(y: torch.Tensor, act: torch.Tensor, w_hot: torch.Tensor,
+                       s_hot: torch.Tensor, align_hot, topk_weights: torch.Tensor | None,
+                       mtk: int, w_cold: torch.Tensor | None = None,
+                       s_cold: torch.Tensor | None = None, align_cold=None) -> None:
+    """down of the split GEMM (npw 4, sk 1) from the bf16 activation [mtk, K]: each
+    workgroup quantizes its block's rows as silu_mul_quant (group 128) does, so y [mtk, N]
+    equals the split GEMM on that kernel's q2 / s2, bit for bit."""
+    N, K = w_hot.shape[1], w_hot.shape[2]
+    assert y.shape == (mtk, N) and y.dtype == torch.bfloat16 and y.is_contiguous()
+    assert act.shape == (mtk, K) and act.dtype == torch.bfloat16 and act.is_contiguous()
+    sh, eh, nh = align_hot
+    sc, ec, nc = align_cold if align_cold is not None else (None, None, None)
+    rc = lib().rlu_moe_gemm_split_qin(
+        _p(act), _p(w_hot), _p(s_hot), _p(sh), _p(eh), _p(nh),
+        _P(device_ptr(w_cold)) if w_cold is not None else _P(0),
+        _P(device_ptr(s_cold)) if s_cold is not None else _P(0), _p(sc), _p(ec), _p(nc),
+        _p(topk_weights), _p(y), sh.numel(), mtk, K, N, _P(stream_ptr()))
+    check(rc, "rlu_moe_gemm_split_qin")
+
+
 def gemm_fp8_block_q(qx: torch.Tensor, xs: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor,
                      out: torch.Tensor | None = None, wv: int = 0, npw: int = 0) -> torch.Tensor:
     """e4m3 [M, K] (xs [M, K/128]) x e4m3 [N, K] in fragment order (ws [N/128, K/128])^T ->

@@ -466,6 +466,108 @@ def test_moe_gemm_split_one_launch_equals_two_calls(pkg, ops, layer):
     assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
 
 
+# ---- gate_up with its activation, down from the activation (decode) -------------------------
+@pytest.mark.parametrize("M,sk,pinned,holes", [(1, 1, False, False), (5, 1, True, False),
+                                               (20, 2, False, False), (20, 2, True, True),
+                                               (20, 4, False, False)])
+def test_moe_gemm_split_act_and_qin_equal_the_unfused_path(pkg, ops, layer, M, sk, pinned,
+                                                            holes):
+    """gate_up with SiLU-mul in its epilogue (rlu_moe_gemm_split_act) equals the split gate_up
+    GEMM followed by silu_mul_quant's activation, and the down GEMM that quantizes that
+    activation per workgroup (rlu_moe_gemm_split_qin) equals the split down GEMM on
+    silu_mul_quant's q2 / s2, bit for bit: hot slots + cold full tensor (device or pinned host
+    memory), and with holes (every other hot block's expert id set to -1, as the gather
+    overlap's resident bucket has them) then the hot list alone over the other blocks."""
+    E, H, I = layer["E"], layer["H"], layer["I"]
+    top_k = 10
+    ids = routing(M, top_k, E, seed=M + 61)
+    mtk = ids.size
+    hot_experts = sorted(set(ids.reshape(-1).tolist()))[::2]
+    hot = {ex: i for i, ex in enumerate(hot_experts)}
+    al = to_dev_i32(*align_all(ids, E, hot))
+    idx = torch.tensor(hot_experts, device=DEV)
+    slots = {n: layer[n][idx].contiguous() for n in ("w13t", "w13s", "w2t", "w2s")}
+    full = {n: layer[n] for n in ("w13t", "w13s", "w2t", "w2s")}
+    if pinned:
+        for n, t in list(full.items()):
+            h = torch.empty(t.shape, dtype=t.dtype, pin_memory=True)
+            h.copy_(t)
+            full[n] = h
+    rng = np.random.default_rng(M + 62)
+    x = fp8.bf16_round(rng.standard_normal((M, H)).astype(np.float32))
+    qx, xs = fp8.group_quant(x, 128)
+    qx_t = torch.from_numpy(qx).to(DEV).view(torch.float8_e4m3fn)
+    xs_t = torch.from_numpy(xs).to(DEV)
+    tw = torch.from_numpy(rng.random(mtk).astype(np.float32)).to(DEV)
+    hot_al, cold_al = al[0:3], al[3:6]
+    passes = [(hot_al, True)]
+    if holes:                      # two hot passes over complementary block sets
+        e = hot_al[1].clone()
+        e_odd = e.clone()
+        e_odd[1::2] = -1
+        e_even = e.clone()
+        e_even[0::2] = -1
+        passes = [((hot_al[0], e_odd, hot_al[2]), True), ((hot_al[0], e_even, hot_al[2]), False)]
+    # the unfused path
+    ic1 = torch.full((mtk, 2 * I), float("nan"), dtype=torch.bfloat16, device=DEV)
+    ic3 = torch.full((mtk, H), float("nan"), dtype=torch.bfloat16, device=DEV)
+    P = ctypes.c_void_p
+    st = P(torch.cuda.current_stream().cuda_stream)
+    def split(y, a, a_s, w, ws, wc, wsc, alh, cold, t, tk, npw, sk_):
+        if not cold:               # the hot list alone: the single-set GEMM
+            run_gemm(ops, y, a, a_s, w, ws, alh, t, mtk, tk, npw=npw, sk=sk_)
+            return
+        rc = pkg.lib().rlu_moe_gemm_split(
+            P(a.data_ptr()), P(a_s.data_ptr()), P(w.data_ptr()), P(ws.data_ptr()),
+            P(alh[0].data_ptr()), P(alh[1].data_ptr()), P(alh[2].data_ptr()),
+            P(pkg._lib.device_ptr(wc)), P(pkg._lib.device_ptr(wsc)),
+            P(cold_al[0].data_ptr()), P(cold_al[1].data_ptr()), P(cold_al[2].data_ptr()),
+            P(0 if t is None else t.data_ptr()), P(y.data_ptr()), alh[0].numel(), mtk, tk,
+            a.shape[1], w.shape[1], 0, sk_, npw, st)
+        assert rc == 0
+    gpu_case(f"split act/qin M={M} sk={sk} pinned={pinned} holes={holes}: unfused")
+    for alh, cold in passes:
+        split(ic1, qx_t, xs_t, slots["w13t"], slots["w13s"], full["w13t"], full["w13s"], alh,
+              cold, None, top_k, 2, sk)
+    act_ref, q2, s2 = ops.silu_mul_quant(ic1, write_act=True)
+    for alh, cold in passes:
+        split(ic3, q2, s2, slots["w2t"], slots["w2s"], full["w2t"], full["w2s"], alh, cold, tw,
+              1, 4, 1)
+    # the fused pair
+    act = torch.full((mtk, I), float("nan"), dtype=torch.bfloat16, device=DEV)
+    y = torch.full((mtk, H), float("nan"), dtype=torch.bfloat16, device=DEV)
+    gpu_case(f"split act/qin M={M} sk={sk} pinned={pinned} holes={holes}: fused")
+    for alh, cold in passes:
+        ops.moe_gemm_split_act(act, qx_t, xs_t, slots["w13t"], slots["w13s"], alh, mtk, top_k,
+                               *((full["w13t"], full["w13s"], cold_al) if cold else ()), sk=sk)
+    for alh, cold in passes:
+        ops.moe_gemm_split_qin(y, act, slots["w2t"], slots["w2s"], alh, tw, mtk,
+                               *((full["w2t"], full["w2s"], cold_al) if cold else ()))
+    torch.cuda.synchronize()
+    assert not torch.isnan(act).any() and not torch.isnan(y).any()
+    assert torch.equal(act.view(torch.int16), act_ref.view(torch.int16))
+    assert torch.equal(y.view(torch.int16), ic3.view(torch.int16))
+
+
+def test_moe_gemm_split_act_qin_return_codes(pkg):
+    """Size checks return before anything is launched (null operands included)."""
+    P = ctypes.c_void_p
+    st = P(torch.cuda.current_stream().cuda_stream)
+    buf = torch.zeros(4096, dtype=torch.int32, device=DEV)
+    b = P(buf.data_ptr())
+    act = pkg.lib().rlu_moe_gemm_split_act
+    qin = pkg.lib().rlu_moe_gemm_split_qin
+    # N not a multiple of 256 / K not a multiple of 128 / K past 1024 / null operands
+    assert act(*([b] * 7), P(0), *([P(0)] * 4), b, 16, 10, 10, 2560, 1408, 0, 0, st) == -2
+    assert act(*([b] * 7), P(0), *([P(0)] * 4), b, 16, 10, 10, 2500, 1536, 0, 0, st) == -2
+    assert act(*([b] * 6), P(0), P(0), *([P(0)] * 4), b, 16, 10, 10, 2560, 1536, 0, 0, st) == -1
+    assert qin(*([b] * 6), P(0), *([P(0)] * 5), b, 16, 10, 1152, 2560, st) == -2
+    assert qin(*([b] * 6), P(0), *([P(0)] * 5), b, 16, 10, 768, 2432, st) == -2
+    assert qin(P(0), *([b] * 5), P(0), *([P(0)] * 5), b, 16, 10, 768, 2560, st) == -1
+    # a cold weight tensor without its align
+    assert qin(*([b] * 6), b, P(0), *([P(0)] * 4), b, 16, 10, 768, 2560, st) == -1
+
+
 # ---- down + moe_sum folded (decode) ----------------------------------------------------------
 @pytest.mark.parametrize("M,pinned", [(1, False), (5, False), (20, False), (20, True)])
 def test_moe_down_sum_equals_split_gemm_and_moe_sum(pkg, ops, layer, M, pinned):
