@@ -7,8 +7,9 @@ weights ~N(0, 0.02) before quantization), S=257 HBM slots per layer warm-started
 hottest experts of each layer's routing, top-10 routing of B=4 streams x 5 rows (MTP-4) = 20
 tokens per step from a seeded Zipf(1.1) trace per layer (seed 1000 + layer, rows correlated so a
 layer sees 5-13 misses per step). Per layer and step: r4d_lru_fused (manager + both aligns),
-group-128 activation quant, gate_up GEMM (hot slots + cold tensor), SiLU-mul-quant, down GEMM
-with routed weights, moe_sum -- captured once as a HIP graph and replayed with new routing.
+group-128 activation quant, gate_up GEMM (hot slots + cold tensor) with the SiLU-mul in its
+epilogue, down GEMM with routed weights (quantizing the activation per workgroup, as
+silu_mul_quant does), moe_sum -- captured once as a HIP graph and replayed with new routing.
 
 `value` is ms per 52-layer step with every input resident in HBM: the miss gather, which reads
 pinned host memory over PCIe, is timed in a second graph and reported as
