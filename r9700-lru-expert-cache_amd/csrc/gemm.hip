@@ -133,10 +133,9 @@ __global__ __launch_bounds__(G * WAVE) void moe_gemm_k(
           constexpr int NP = (QIN_MAXG + GS - 1) / GS;
           uint4 raw[NP];
 #pragma unroll
-          for (int p = 0; p < NP; ++p)              // padding rows are zeros, not loaded
-            raw[p] = (ok && g0 + p * GS < ng)
-                         ? *reinterpret_cast<const uint4*>(src + (g0 + p * GS) * 128)
-                         : uint4{0u, 0u, 0u, 0u};
+          for (int p = 0; p < NP; ++p)
+            if (g0 + p * GS < ng)
+              raw[p] = *reinterpret_cast<const uint4*>(src + (g0 + p * GS) * 128);
 #pragma unroll
           for (int p = 0; p < NP; ++p) {
             const int g = g0 + p * GS;
