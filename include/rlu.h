@@ -241,6 +241,17 @@ int rlu_moe_down_sum(const void* q2, const float* s2, const int* topk_ids,
                      const float* s_hot, const void* w_full, const float* s_full, void* out,
                      int M, int top_k, int K, int N, int E, hipStream_t stream);
 
+/* No counterpart in the reference (see rlu_moe_down_sum; the reference quantizes the activation
+ * in its own launch, kernels/fused_silu_mul_quant.py:75-101): rlu_moe_down_sum from the bf16
+ * SiLU-mul activation act [M top_k, K] (rlu_moe_gemm_split_act's output) instead of q2 / s2.
+ * Each workgroup quantizes its token's rows per 128-column group exactly as rlu_silu_mul_quant
+ * (group 128) does, so out equals rlu_moe_down_sum on that kernel's q2 / s2, bit for bit. Same
+ * limits and return codes. */
+int rlu_moe_down_sum_act(const void* act, const int* topk_ids, const float* topk_weights,
+                         const int* table, const void* w_hot, const float* s_hot,
+                         const void* w_full, const float* s_full, void* out, int M, int top_k,
+                         int K, int N, int E, hipStream_t stream);
+
 /* No counterpart in the reference. For callers that cannot allocate -- code recorded into a HIP
  * graph, serving loops and harnesses that forbid hipMalloc: rlu_moe_gemm_tiles followed by
  * rlu_moe_gemm_fp8blk_tiled (same kernels, same results bit for bit) with the tile list kept in

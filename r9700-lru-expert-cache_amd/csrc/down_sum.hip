@@ -21,6 +21,7 @@
 
 #include "gemm_common.h"
 #include "numerics.h"
+#include "quant_row.h"
 #include "wave.h"
 
 namespace rlu {
@@ -31,15 +32,22 @@ constexpr int BUF_WORD3 = 0x00020000;      // raw buffer descriptor word 3 on gf
 constexpr int NTP = 2;                     // buffer cache policy: streaming
 constexpr int MAXK = 16;                   // top_k the kernel takes (A rows of one MFMA)
 
-template <int NS, int W, int TK>
+// ACT: qa is the bf16 activation [M top_k, K] (the SiLU-mul output) and sa is not read; the
+// workgroup quantizes the token's rows per 128-column group into LDS first, exactly as
+// silu_mul_quant_g128_k does (same amax, scale and rounding), and the waves take their A
+// fragments and the rows' scales from there.
+template <int NS, int W, int TK, bool ACT = false>
 __global__ __launch_bounds__(W * WAVE) void down_sum_k(
-    const uint8_t* __restrict__ qa, const float* __restrict__ sa, const int* __restrict__ ids,
+    const void* __restrict__ qa, const float* __restrict__ sa, const int* __restrict__ ids,
     const float* __restrict__ tw, const int* __restrict__ table,
     const uint8_t* __restrict__ hw, const float* __restrict__ hs,
     const uint8_t* __restrict__ cw, const float* __restrict__ cs,
     uint16_t* __restrict__ out, int M, int N, int E) {
   constexpr int K = NS * 128;
   static_assert(TK <= MAXK, "top_k rows fit one MFMA");
+  constexpr int ALS = K + 16;                      // ACT: LDS row stride of the quantized rows
+  __shared__ uint8_t alds[ACT ? TK * ALS : 16];
+  __shared__ float xsl[ACT ? TK * NS : 4];
   const int lane = lane_id(), w = uniform((int)(threadIdx.x / WAVE));
   const int r16 = lane & 15, c4 = lane >> 4;
   // workgroup -> (token, column group): the tokens of one column group are consecutive within
@@ -68,11 +76,14 @@ __global__ __launch_bounds__(W * WAVE) void down_sum_k(
   // the token's A rows: row r16 of the MFMA is (t, k = r16); rows past top_k repeat row 0
   const int arow = t * TK + (r16 < TK ? r16 : 0);
   v4u ra[NS][2];
+  if constexpr (!ACT) {
 #pragma unroll
-  for (int j = 0; j < NS; ++j) {
-    const uint8_t* p = qa + (size_t)arow * K + j * 128 + 16 * c4;
-    ra[j][0] = *reinterpret_cast<const v4u*>(p);
-    ra[j][1] = *reinterpret_cast<const v4u*>(p + 64);
+    for (int j = 0; j < NS; ++j) {
+      const uint8_t* p = reinterpret_cast<const uint8_t*>(qa) + (size_t)arow * K + j * 128 +
+                         16 * c4;
+      ra[j][0] = *reinterpret_cast<const v4u*>(p);
+      ra[j][1] = *reinterpret_cast<const v4u*>(p + 64);
+    }
   }
   v4u rb[NS][2];
   const int voff = lane * 16;
@@ -92,13 +103,52 @@ __global__ __launch_bounds__(W * WAVE) void down_sum_k(
     const int kk = k < TK ? k : TK - 1;
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
-      fx[q][j] = sa[(size_t)(t * TK + kk) * NS + j];
+      if constexpr (ACT)                           // row kk's scale, from LDS
+        fx[q][j] = xsl[kk * NS + j];
+      else
+        fx[q][j] = sa[(size_t)(t * TK + kk) * NS + j];
       fw[q][j] = sp[kk][j];
     }
   };
-  load_scales(0, 0);
 #pragma unroll
   for (int j = 0; j < NS; ++j) issue(j, wbuf(0));
+  if constexpr (ACT) {
+    // the workgroup quantizes the token's top_k rows into LDS once, while the first expert's
+    // weights are in flight: 16-lane group q takes (row, 128-column group) pairs q, q + NG, ...
+    // and lane l16 columns [8 l16, 8 l16 + 8) of each, as silu_mul_quant_g128_k does
+    constexpr int NG = W * WAVE / 16, NPR = TK * NS, NPASS = (NPR + NG - 1) / NG;
+    const int q16 = (int)threadIdx.x / 16, l16 = lane & 15;
+    const uint16_t* act = reinterpret_cast<const uint16_t*>(qa) + (size_t)t * TK * K;
+    uint4 raw[NPASS];
+#pragma unroll
+    for (int p = 0; p < NPASS; ++p) {
+      const int pr = q16 + p * NG, r = pr / NS, g = pr - r * NS;
+      if (pr < NPR)
+        raw[p] = *reinterpret_cast<const uint4*>(act + (size_t)r * K + g * 128 + 8 * l16);
+    }
+#pragma unroll
+    for (int p = 0; p < NPASS; ++p) {
+      const int pr = q16 + p * NG, r = pr / NS, g = pr - r * NS;
+      if (pr < NPR) {                              // uniform over each 16-lane group
+        float v[8];
+        unpack8_bf16(raw[p], v);
+        uint32_t m = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) m = max(m, abs_bits(v[i]));
+        const float sc = scale_of(row_max_u32(m));
+        *reinterpret_cast<uint2*>(alds + r * ALS + g * 128 + 8 * l16) = quant8(v, sc);
+        if (l16 == 0) xsl[r * NS + g] = sc;
+      }
+    }
+    __syncthreads();
+    const int ar = r16 < TK ? r16 : 0;
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+      ra[j][0] = *reinterpret_cast<const v4u*>(alds + ar * ALS + j * 128 + 16 * c4);
+      ra[j][1] = *reinterpret_cast<const v4u*>(alds + ar * ALS + j * 128 + 64 + 16 * c4);
+    }
+  }
+  load_scales(0, 0);
   float sum = 0.f;
 #pragma unroll
   for (int k = 0; k < TK; ++k) {
@@ -145,10 +195,31 @@ int rlu_moe_down_sum(const void* q2, const float* s2, const int* topk_ids,
   if (M == 0) return 0;
   constexpr int W = 4;
   const int grid = M * (N / (16 * W));
-  hipLaunchKernelGGL((dsum::down_sum_k<6, W, 10>), dim3(grid), dim3(W * WAVE), 0, stream,
-                     (const uint8_t*)q2, s2, topk_ids, topk_weights, table,
-                     (const uint8_t*)w_hot, s_hot, (const uint8_t*)w_full, s_full,
-                     (uint16_t*)out, M, N, E);
+  hipLaunchKernelGGL((dsum::down_sum_k<6, W, 10>), dim3(grid), dim3(W * WAVE), 0, stream, q2,
+                     s2, topk_ids, topk_weights, table, (const uint8_t*)w_hot, s_hot,
+                     (const uint8_t*)w_full, s_full, (uint16_t*)out, M, N, E);
+  return (int)hipGetLastError();
+}
+
+// rlu_moe_down_sum from the bf16 SiLU-mul activation act [M top_k, K] instead of q2 / s2: the
+// kernel quantizes each token's rows as silu_mul_quant (group 128) does, so out is the same
+// bit for bit. Same limits and codes. No counterpart in the reference; see include/rlu.h.
+int rlu_moe_down_sum_act(const void* act, const int* topk_ids, const float* topk_weights,
+                         const int* table, const void* w_hot, const float* s_hot,
+                         const void* w_full, const float* s_full, void* out, int M, int top_k,
+                         int K, int N, int E, hipStream_t stream) {
+  using namespace rlu;
+  if (M < 0 || top_k < 1 || top_k > dsum::MAXK || K <= 0 || N <= 0 || E <= 0) return -1;
+  if (!act || !topk_ids || !topk_weights || !table || !w_full || !s_full || !out) return -1;
+  if (K % 128 || N % 128) return -2;
+  if (K != 768 || top_k != 10) return -6;
+  if (N % 64) return -2;
+  if (M == 0) return 0;
+  constexpr int W = 4;
+  const int grid = M * (N / (16 * W));
+  hipLaunchKernelGGL((dsum::down_sum_k<6, W, 10, true>), dim3(grid), dim3(W * WAVE), 0, stream,
+                     act, nullptr, topk_ids, topk_weights, table, (const uint8_t*)w_hot, s_hot,
+                     (const uint8_t*)w_full, s_full, (uint16_t*)out, M, N, E);
   return (int)hipGetLastError();
 }
 

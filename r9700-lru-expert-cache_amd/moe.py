@@ -88,11 +88,11 @@ class LruMoELayer:
 
         fuse_act (decode): gate_up writes the SiLU-mul activation from its epilogue
         (ops.moe_gemm_split_act) and down quantizes it per workgroup
-        (ops.moe_gemm_split_qin), in place of gate_up into ic1, silu_mul_quant and down on
-        q2 / s2: the same output bit for bit, one launch fewer per layer (two with the gather
-        overlap). Default on for decode layers that do not fold down and moe_sum, at npw 2 / 4,
-        sk2 = 1, wv = 0, 2 I % 256 == 0, hidden % 256 == 0 and I <= 1024; prefill layers fuse
-        the activation into their own gate_up."""
+        (ops.moe_gemm_split_qin, or ops.moe_down_sum_act where down and moe_sum are folded),
+        in place of gate_up into ic1, silu_mul_quant and down on q2 / s2: the same output bit
+        for bit, one launch fewer per layer (two with the gather overlap). Default on for
+        decode layers at npw 2 / 4, sk2 = 1, wv = 0, 2 I % 256 == 0, hidden % 256 == 0 and
+        I <= 1024; prefill layers fuse the activation into their own gate_up."""
         dev = torch.device(device)
         self.full = full
         self.full_ptrs = full.ptrs()
@@ -142,10 +142,9 @@ class LruMoELayer:
         self.fuse_act = self.prefill and ops.moe_gemm_tiled_silu_quant_built(self.H, self.N1)
         # decode: gate_up with its activation, down quantizing it (no activation launch)
         if fuse_act is None:
-            fuse_act = (not self.prefill and not self.fold_sum and npw1 == 2 and npw2 == 4
-                        and sk2 == 1 and wv == 0 and self.N1 % 256 == 0
-                        and self.H % 256 == 0 and self.I <= 1024)
-        self.fuse_dec = bool(fuse_act) and not self.prefill and not self.fold_sum
+            fuse_act = (not self.prefill and npw1 == 2 and npw2 == 4 and sk2 == 1 and wv == 0
+                        and self.N1 % 256 == 0 and self.H % 256 == 0 and self.I <= 1024)
+        self.fuse_dec = bool(fuse_act) and not self.prefill
         self.act = (torch.empty((self.mtk, self.I), dtype=torch.bfloat16, device=dev)
                     if self.fuse_dec else None)
         self.ic1 = (None if self.fuse_act or self.fuse_dec else
@@ -365,9 +364,12 @@ class LruMoELayer:
                 if ids.dtype != torch.int32 or not ids.is_contiguous():
                     self.ids32.copy_(ids)
                     ids = self.ids32
-                ops.moe_down_sum(self.q2, self.s2, ids, tw.view(M, self.top_k),
-                                 self.cache.table, self.slots.w2, self.slots.s2, self.full.w2,
-                                 self.full.s2, output)
+                w = (self.cache.table, self.slots.w2, self.slots.s2, self.full.w2, self.full.s2,
+                     output)
+                if self.fuse_dec:                  # the folded down quantizes the activation
+                    ops.moe_down_sum_act(self.act, ids, tw.view(M, self.top_k), *w)
+                else:
+                    ops.moe_down_sum(self.q2, self.s2, ids, tw.view(M, self.top_k), *w)
                 return
             self._down(tw)
         ops.moe_sum(self.ic3.view(M, self.top_k, self.H), output)

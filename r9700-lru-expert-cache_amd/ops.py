@@ -110,6 +110,27 @@ def moe_down_sum(q2: torch.Tensor, s2: torch.Tensor, topk_ids: torch.Tensor,
     check(rc, "rlu_moe_down_sum")
 
 
+def moe_down_sum_act(act: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor,
+                     table: torch.Tensor, w_hot: torch.Tensor, s_hot: torch.Tensor,
+                     w_full: torch.Tensor, s_full: torch.Tensor, out: torch.Tensor) -> None:
+    """moe_down_sum from the bf16 SiLU-mul activation act [M top_k, K] (what
+    moe_gemm_split_act writes) in place of silu_mul_quant's q2 / s2: the kernel quantizes each
+    token's rows per 128-column group as silu_mul_quant does, so out is the same bit for bit
+    and the activation needs no quant launch of its own."""
+    M, top_k = topk_ids.shape
+    N, K = w_full.shape[1], w_full.shape[2]
+    assert topk_ids.dtype == torch.int32 and topk_ids.is_contiguous()
+    assert topk_weights.dtype == torch.float32 and topk_weights.is_contiguous()
+    assert topk_weights.shape == (M, top_k) and act.shape == (M * top_k, K)
+    assert act.dtype == torch.bfloat16 and act.is_contiguous()
+    assert out.shape == (M, N) and out.dtype == torch.bfloat16 and out.is_contiguous()
+    rc = lib().rlu_moe_down_sum_act(
+        _p(act), _p(topk_ids), _p(topk_weights), _p(table), _p(w_hot), _p(s_hot),
+        _P(device_ptr(w_full)), _P(device_ptr(s_full)), _p(out), M, top_k, K, N,
+        w_full.shape[0], _P(stream_ptr()))
+    check(rc, "rlu_moe_down_sum_act")
+
+
 def _r4d_fp8_moe_gemm_into(y: torch.Tensor, qx: torch.Tensor, x_scale: torch.Tensor,
                            wq: torch.Tensor, ws_t: torch.Tensor, wref: torch.Tensor | None,
                            sorted_ids: torch.Tensor, expert_ids: torch.Tensor,

@@ -639,6 +639,61 @@ def test_moe_down_sum_return_codes(pkg):
     assert f(P(0), p, p, p, p, p, p, p, p, p, 4, 10, 768, 2560, 64, s) == -1
 
 
+@pytest.mark.parametrize("M,pinned", [(1, False), (5, False), (5, True), (8, False)])
+def test_moe_down_sum_act_equals_down_sum_on_silu_quant(pkg, ops, layer, M, pinned):
+    """The folded down + moe_sum from the bf16 SiLU-mul activation (each workgroup quantizes
+    its token's rows) equals the folded kernel on silu_mul_quant's q2 / s2 of the same gate_up
+    output, bit for bit: hot slots + cold full tensor in device or pinned host memory, with an
+    all-zero token (its scales fall to the floor 1 / (448 * 512)) and one of large values."""
+    E, H, I = layer["E"], layer["H"], layer["I"]
+    top_k = 10
+    ids = routing(M, top_k, E, seed=M + 93)
+    mtk = ids.size
+    hot_experts = sorted(set(ids.reshape(-1).tolist()))[::2]
+    table = np.full(E, -1, np.int32)
+    for sl, ex in enumerate(hot_experts):
+        table[ex] = sl
+    idx = torch.tensor(hot_experts, device=DEV)
+    sq, ss = layer["w2t"][idx].contiguous(), layer["w2s"][idx].contiguous()
+    fq, fs = layer["w2t"], layer["w2s"]
+    if pinned:
+        fq = torch.empty(fq.shape, dtype=fq.dtype, pin_memory=True); fq.copy_(layer["w2t"])
+        fs = torch.empty(fs.shape, dtype=fs.dtype, pin_memory=True); fs.copy_(layer["w2s"])
+    rng = np.random.default_rng(M + 94)
+    ic1 = rng.standard_normal((mtk, 2 * I)).astype(np.float32)
+    ic1[:top_k] = 0.0                                      # token 0: a zero activation
+    if M > 1:
+        ic1[top_k:2 * top_k] *= 300.0                      # token 1: large values
+    ic1_t = torch.from_numpy(ic1).to(torch.bfloat16).to(DEV)
+    act, q2, s2 = ops.silu_mul_quant(ic1_t, write_act=True)
+    tw = torch.from_numpy(rng.random((M, top_k)).astype(np.float32)).to(DEV)
+    ids_t = torch.from_numpy(ids.astype(np.int32)).to(DEV)
+    table_t = torch.from_numpy(table).to(DEV)
+    want = torch.full((M, H), float("nan"), dtype=torch.bfloat16, device=DEV)
+    got = torch.full_like(want, float("nan"))
+    gpu_case(f"down + moe_sum folded on q2 M={M} pinned={pinned}")
+    ops.moe_down_sum(q2, s2, ids_t, tw, table_t, sq, ss, fq, fs, want)
+    gpu_case(f"down + moe_sum folded on act M={M} pinned={pinned}")
+    ops.moe_down_sum_act(act, ids_t, tw, table_t, sq, ss, fq, fs, got)
+    torch.cuda.synchronize()
+    assert not torch.isnan(want).any()
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+def test_moe_down_sum_act_return_codes(pkg):
+    """Argument errors of the activation form return before anything is launched."""
+    P = ctypes.c_void_p
+    f = pkg.lib().rlu_moe_down_sum_act
+    x = torch.empty(1 << 16, dtype=torch.uint8, device=DEV)
+    p = P(x.data_ptr())
+    s = P(torch.cuda.current_stream().cuda_stream)
+    assert f(p, p, p, p, p, p, p, p, p, 4, 10, 1024, 2560, 64, s) == -6
+    assert f(p, p, p, p, p, p, p, p, p, 4, 8, 768, 2560, 64, s) == -6
+    assert f(p, p, p, p, p, p, p, p, p, 4, 17, 768, 2560, 64, s) == -1
+    assert f(p, p, p, p, p, p, p, p, p, 4, 10, 768, 2500, 64, s) == -2
+    assert f(P(0), p, p, p, p, p, p, p, p, 4, 10, 768, 2560, 64, s) == -1
+
+
 # ---- a tensor-parallel rank's shapes ----------------------------------------------------------
 @pytest.mark.parametrize("which", ["gate_up", "down"])
 def test_moe_gemm_tp2_shapes(ops, which):
