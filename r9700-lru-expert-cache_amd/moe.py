@@ -81,8 +81,9 @@ class LruMoELayer:
         for bit. The reference runs prefill chunks through the same split path
         (r4d_mxfp4_moe.py.lru.diff:659-696; tests/lru/test_numerics_prod.py:44-48).
 
-        fold_sum: run down and moe_sum as one token-major kernel (ops.moe_down_sum, the same
-        output bit for bit) when the gather is not overlapped; default on up to
+        fold_sum: run down and moe_sum as one token-major kernel (ops.moe_down_sum, or
+        ops.moe_down_sum_act from the activation with fuse_act; the same output bit for bit)
+        when the gather is not overlapped; default on up to
         FOLD_SUM_TOKENS tokens at the shapes the kernel is built for (intermediate 768,
         top-10).
 
