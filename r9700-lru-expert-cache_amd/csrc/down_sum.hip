@@ -15,7 +15,8 @@
 // slot, any other from the full tensor (device or pinned host memory).
 //
 // Each expert strip is read once per token that routes to it; workgroups are laid out so that
-// the tokens of one column range run on one XCD at the same time and share its L2.
+// the tokens of one column range run on one XCD at the same time and share its L2. The ACT form
+// takes the bf16 SiLU-mul activation and quantizes it itself (no silu_mul_quant launch).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -113,8 +114,9 @@ __global__ __launch_bounds__(W * WAVE) void down_sum_k(
 #pragma unroll
   for (int j = 0; j < NS; ++j) issue(j, wbuf(0));
   if constexpr (ACT) {
-    // the workgroup quantizes the token's top_k rows into LDS once, while the first expert's
-    // weights are in flight: 16-lane group q takes (row, 128-column group) pairs q, q + NG, ...
+    // the workgroup quantizes the token's top_k rows into LDS once, after the first expert's
+    // weight loads are issued (the wait for the rows covers those loads too: the counter
+    // retires in order): 16-lane group q takes (row, 128-column group) pairs q, q + NG, ...
     // and lane l16 columns [8 l16, 8 l16 + 8) of each, as silu_mul_quant_g128_k does
     constexpr int NG = W * WAVE / 16, NPR = TK * NS, NPASS = (NPR + NG - 1) / NG;
     const int q16 = (int)threadIdx.x / 16, l16 = lane & 15;
