@@ -111,23 +111,26 @@ __global__ __launch_bounds__(W * WAVE) void down_sum_k(
       fw[q][j] = sp[kk][j];
     }
   };
-#pragma unroll
-  for (int j = 0; j < NS; ++j) issue(j, wbuf(0));
+  // ACT: the workgroup quantizes the token's top_k rows into LDS once. The rows' loads go out
+  // before the first expert's weight loads, so that waiting for them (the counter retires in
+  // order) does not wait for the weights: the quant runs while those are in flight. 16-lane
+  // group q takes (row, 128-column group) pairs q, q + NG, ... and lane l16 columns
+  // [8 l16, 8 l16 + 8) of each, as silu_mul_quant_g128_k does.
+  constexpr int NG = W * WAVE / 16, NPR = TK * NS, NPASS = (NPR + NG - 1) / NG;
+  const int q16 = (int)threadIdx.x / 16, l16 = lane & 15;
+  uint4 raw[ACT ? NPASS : 1];
   if constexpr (ACT) {
-    // the workgroup quantizes the token's top_k rows into LDS once, after the first expert's
-    // weight loads are issued (the wait for the rows covers those loads too: the counter
-    // retires in order): 16-lane group q takes (row, 128-column group) pairs q, q + NG, ...
-    // and lane l16 columns [8 l16, 8 l16 + 8) of each, as silu_mul_quant_g128_k does
-    constexpr int NG = W * WAVE / 16, NPR = TK * NS, NPASS = (NPR + NG - 1) / NG;
-    const int q16 = (int)threadIdx.x / 16, l16 = lane & 15;
     const uint16_t* act = reinterpret_cast<const uint16_t*>(qa) + (size_t)t * TK * K;
-    uint4 raw[NPASS];
 #pragma unroll
     for (int p = 0; p < NPASS; ++p) {
       const int pr = q16 + p * NG, r = pr / NS, g = pr - r * NS;
       if (pr < NPR)
         raw[p] = *reinterpret_cast<const uint4*>(act + (size_t)r * K + g * 128 + 8 * l16);
     }
+  }
+#pragma unroll
+  for (int j = 0; j < NS; ++j) issue(j, wbuf(0));
+  if constexpr (ACT) {
 #pragma unroll
     for (int p = 0; p < NPASS; ++p) {
       const int pr = q16 + p * NG, r = pr / NS, g = pr - r * NS;
