@@ -36,7 +36,8 @@
 namespace rlu {
 
 constexpr int GWV = 4;      // waves per workgroup
-constexpr int QIN_MAXG = 8;   // 128-column groups of the activation MODE 2 reads (K <= 1024)
+constexpr int QIN_MAXG = 6;   // 128-column groups of the activation MODE 2 reads (K <= 768):
+                              // its rows' loads stay live across the first weight steps
 constexpr int QIN_G = 4;      // waves per workgroup in MODE 2 (items of one block): with 8,
                               // 40 column tiles x 48 blocks leave CUs idle at B=4 (3.68 ms
                               // per 52-layer step against 3.57)
@@ -118,24 +119,30 @@ __global__ __launch_bounds__(G * WAVE) void moe_gemm_k(
       // MODE 2: the G items of the workgroup share block b (ntiles % G == 0, no item past
       // nitems), so the workgroup quantizes the block's 16 rows into LDS together -- 16-lane
       // group q takes row q % 16 and every (G / 4)-th 128-column group from q / 16 on, lane
-      // l16 columns [8 l16, 8 l16 + 8) of each -- once its item's first weight steps are in
-      // flight; then one workgroup barrier
+      // l16 columns [8 l16, 8 l16 + 8) of each. The rows' loads go out before the item's first
+      // weight steps (pre), so that waiting for them does not wait for the weights (the
+      // counter retires in order); the quant runs while the weights are in flight (pro), then
+      // one workgroup barrier
       constexpr int GS = G / 4;                     // 128-column group stride of a 16-lane group
       static_assert(G % 4 == 0 && SKW == 1, "16-lane groups cover the block's 16 rows");
       const int q16 = (int)threadIdx.x / 16, r = q16 % 16, g0 = q16 / 16;
       const int l16 = lane & 15, ng = K / 128;
       const int sr = sids[b * 16 + r];
-      auto pro = [&]() __attribute__((always_inline)) {
+      const bool ok = sr < mtk;
+      const uint16_t* src =
+          reinterpret_cast<const uint16_t*>(qx) + (size_t)(ok ? sr : 0) * K + 8 * l16;
+      constexpr int NP = (QIN_MAXG + GS - 1) / GS;
+      uint4 raw[NP];
+      auto pre = [&]() __attribute__((always_inline)) {   // the rows' loads, ahead of weights
         if (eid >= 0) {
-          const bool ok = sr < mtk;
-          const uint16_t* src =
-              reinterpret_cast<const uint16_t*>(qx) + (size_t)(ok ? sr : 0) * K + 8 * l16;
-          constexpr int NP = (QIN_MAXG + GS - 1) / GS;
-          uint4 raw[NP];
 #pragma unroll
           for (int p = 0; p < NP; ++p)
             if (g0 + p * GS < ng)
               raw[p] = *reinterpret_cast<const uint4*>(src + (g0 + p * GS) * 128);
+        }
+      };
+      auto pro = [&]() __attribute__((always_inline)) {
+        if (eid >= 0) {
 #pragma unroll
           for (int p = 0; p < NP; ++p) {
             const int g = g0 + p * GS;
@@ -159,9 +166,11 @@ __global__ __launch_bounds__(G * WAVE) void moe_gemm_k(
       if (live)
         item_mma<NPW, SKW, DENSE, ring_of(NPW), PAIR, AL>(qx, xs, wq, ws, so, eid, n0, tw, mtk,
                                                           top_k, K, N, ks, sx, acc, sod, twv,
-                                                          alds, als, xsl, pro);
-      else
+                                                          alds, als, xsl, pro, pre);
+      else {
+        pre();
         pro();
+      }
     } else if (live) {
       item_mma<NPW, SKW, DENSE, ring_of(NPW), PAIR, AL>(qx, xs, wq, ws, so, eid, n0, tw, mtk,
                                                         top_k, K, N, ks, sx, acc, sod, twv);
@@ -376,7 +385,7 @@ int rlu_moe_gemm_split_act(const void* qx, const float* xs, const void* wq_hot,
 // output): each workgroup quantizes its block's rows per 128-column group as silu_mul_quant
 // does (same scales and codes) and runs the down GEMM on them, so y equals
 // rlu_moe_gemm_split (npw 4, sk 1) on silu_mul_quant's q2 / s2, bit for bit. Routed weights
-// as there; wq == NULL runs the hot list alone. K <= 1024, N % 256 == 0.
+// as there; wq == NULL runs the hot list alone. K <= 768, N % 256 == 0.
 int rlu_moe_gemm_split_qin(const void* act, const void* wq_hot, const float* ws_hot,
                            const int* sorted_hot, const int* eids_hot, const int* npad_hot,
                            const void* wq, const float* ws, const int* sorted_cold,

@@ -39,14 +39,15 @@ __host__ __device__ __forceinline__ int item_steps(int K) {
 // the others the matching up columns N / 2 + n0 + 16 (s - NPW / 2), each half with its own
 // weight-block scales, so a lane holds gate and up of the same (row, column).
 // AL: the A operand is the block's 16 rows in LDS (alds: row r at r * als bytes, xsl: their
-// K / 128 scales per row), for SKW = 1; qx / xs are not read. pro() runs once the first D
-// weight steps are in flight and before anything reads LDS: with AL it fills alds / xsl.
+// K / 128 scales per row), for SKW = 1; qx / xs are not read. pre() runs before the first
+// weight loads are issued (loads that must not queue behind them), pro() once the first D
+// weight steps are in flight and before anything reads LDS: with AL they fill alds / xsl.
 struct NoPro {
   __device__ void operator()() const {}
 };
 
 template <int NPW, int SKW, bool DENSE, int D = ring_of(NPW), bool PAIR = false, bool AL = false,
-          class PRO = NoPro>
+          class PRO = NoPro, class PRE = NoPro>
 __device__ __forceinline__ void item_mma(const uint8_t* __restrict__ qx,
                                          const float* __restrict__ xs,
                                          const uint8_t* __restrict__ wq,
@@ -56,7 +57,8 @@ __device__ __forceinline__ void item_mma(const uint8_t* __restrict__ qx,
                                          int N, int ks, float* sx, v4f (&acc)[NPW],
                                          int (&sod)[4], float (&twv)[4],
                                          const uint8_t* alds = nullptr, int als = 0,
-                                         const float* xsl = nullptr, const PRO& pro = PRO()) {
+                                         const float* xsl = nullptr, const PRO& pro = PRO(),
+                                         const PRE& pre = PRE()) {
   static_assert(!PAIR || (NPW % 2 == 0 && !DENSE), "gate / up pairs");
   static_assert(!AL || (SKW == 1 && !DENSE), "A from LDS: one wave per item");
   constexpr int NH = PAIR ? 2 : 1;                  // weight-scale rows per item
@@ -116,8 +118,11 @@ __device__ __forceinline__ void item_mma(const uint8_t* __restrict__ qx,
 #pragma unroll
     for (int h = 0; h < NH; ++h)
       f[h] = *reinterpret_cast<const v4f*>(sx + (k * NH + h) * 16 + 4 * c4);
-    const v8i av = AL ? pack8(*reinterpret_cast<const v4u*>(A + k * 128),
-                              *reinterpret_cast<const v4u*>(A + k * 128 + 64))
+    // ring padding (k >= kpw, scale 0) reads the last real step's A, as the register path
+    // does: the LDS past a row's K bytes is not the row's (0 x a NaN code would be NaN)
+    const int ka = k < kpw ? k : kpw - 1;
+    const v8i av = AL ? pack8(*reinterpret_cast<const v4u*>(A + ka * 128),
+                              *reinterpret_cast<const v4u*>(A + ka * 128 + 64))
                       : pack8(ra[j][0], ra[j][1]);
 #pragma unroll
     for (int s = 0; s < NPW; ++s) {
@@ -127,6 +132,7 @@ __device__ __forceinline__ void item_mma(const uint8_t* __restrict__ qx,
       for (int i = 0; i < 4; ++i) acc[s][i] = fmaf(d[i], f[h][i], acc[s][i]);
     }
   };
+  pre();
 #pragma unroll
   for (int j = 0; j < D; ++j) issue(j, min(j, kpw - 1));
   pro();

@@ -93,7 +93,7 @@ class LruMoELayer:
         in place of gate_up into ic1, silu_mul_quant and down on q2 / s2: the same output bit
         for bit, one launch fewer per layer (two with the gather overlap). Default on for
         decode layers at npw 2 / 4, sk2 = 1, wv = 0, 2 I % 256 == 0, hidden % 256 == 0 and
-        I <= 1024; prefill layers fuse the activation into their own gate_up."""
+        I <= 768; prefill layers fuse the activation into their own gate_up."""
         dev = torch.device(device)
         self.full = full
         self.full_ptrs = full.ptrs()
@@ -144,7 +144,7 @@ class LruMoELayer:
         # decode: gate_up with its activation, down quantizing it (no activation launch)
         if fuse_act is None:
             fuse_act = (not self.prefill and npw1 == 2 and npw2 == 4 and sk2 == 1 and wv == 0
-                        and self.N1 % 256 == 0 and self.H % 256 == 0 and self.I <= 1024)
+                        and self.N1 % 256 == 0 and self.H % 256 == 0 and self.I <= 768)
         self.fuse_dec = bool(fuse_act) and not self.prefill
         self.act = (torch.empty((self.mtk, self.I), dtype=torch.bfloat16, device=dev)
                     if self.fuse_dec else None)

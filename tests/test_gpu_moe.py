@@ -562,6 +562,7 @@ def test_moe_gemm_split_act_qin_return_codes(pkg):
     assert act(*([b] * 7), P(0), *([P(0)] * 4), b, 16, 10, 10, 2500, 1536, 0, 0, st) == -2
     assert act(*([b] * 6), P(0), P(0), *([P(0)] * 4), b, 16, 10, 10, 2560, 1536, 0, 0, st) == -1
     assert qin(*([b] * 6), P(0), *([P(0)] * 5), b, 16, 10, 1152, 2560, st) == -2
+    assert qin(*([b] * 6), P(0), *([P(0)] * 5), b, 16, 10, 896, 2560, st) == -2   # K > 768
     assert qin(*([b] * 6), P(0), *([P(0)] * 5), b, 16, 10, 768, 2432, st) == -2
     assert qin(P(0), *([b] * 5), P(0), *([P(0)] * 5), b, 16, 10, 768, 2560, st) == -1
     # a cold weight tensor without its align
