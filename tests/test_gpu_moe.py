@@ -549,6 +549,60 @@ def test_moe_gemm_split_act_and_qin_equal_the_unfused_path(pkg, ops, layer, M, s
     assert torch.equal(y.view(torch.int16), ic3.view(torch.int16))
 
 
+@pytest.mark.parametrize("I", [128, 256, 640])
+def test_moe_gemm_split_act_qin_short_k(pkg, ops, I):
+    """The decode pair at intermediates whose K steps do not fill the register ring (down's K =
+    I: 1, 2 and 5 steps against a ring of 3, so the ring is padded with scale-0 steps): gate_up
+    with its activation and down quantizing it equal the unfused split GEMMs around
+    silu_mul_quant bit for bit, hot slots + cold tensor, and no output is NaN. A padded step
+    once read its LDS A operand past the row's bytes."""
+    E, H, M, top_k = 24, 512, 20, 10
+    w13, s13 = make_experts(E, 2 * I, H, 300 + I)
+    w2, s2w = make_experts(E, H, I, 400 + I)
+    w13t, w2t = ops.shuffle_fp8_weight(w13), ops.shuffle_fp8_weight(w2)
+    ids = routing(M, top_k, E, seed=I)
+    mtk = ids.size
+    hot_experts = sorted(set(ids.reshape(-1).tolist()))[::2]
+    hot = {ex: i for i, ex in enumerate(hot_experts)}
+    al = to_dev_i32(*align_all(ids, E, hot))
+    idx = torch.tensor(hot_experts, device=DEV)
+    rng = np.random.default_rng(I + 1)
+    x = fp8.bf16_round(rng.standard_normal((M, H)).astype(np.float32))
+    qx, xs = fp8.group_quant(x, 128)
+    qx_t = torch.from_numpy(qx).to(DEV).view(torch.float8_e4m3fn)
+    xs_t = torch.from_numpy(xs).to(DEV)
+    tw = torch.from_numpy(rng.random(mtk).astype(np.float32)).to(DEV)
+    P = ctypes.c_void_p
+    st = P(torch.cuda.current_stream().cuda_stream)
+
+    hs = [t[idx].contiguous() for t in (w13t, s13, w2t, s2w)]     # the hot slots
+
+    def split(y, a, a_s, hw, hws, wt, ws, t, tk, npw, sk):
+        rc = pkg.lib().rlu_moe_gemm_split(
+            P(a.data_ptr()), P(a_s.data_ptr()), P(hw.data_ptr()), P(hws.data_ptr()),
+            P(al[0].data_ptr()), P(al[1].data_ptr()), P(al[2].data_ptr()), P(wt.data_ptr()),
+            P(ws.data_ptr()), P(al[3].data_ptr()), P(al[4].data_ptr()), P(al[5].data_ptr()),
+            P(0 if t is None else t.data_ptr()), P(y.data_ptr()), al[0].numel(), mtk, tk,
+            a.shape[1], wt.shape[1], 0, sk, npw, st)
+        assert rc == 0
+    gpu_case(f"short-K pair I={I}: unfused")
+    ic1 = torch.full((mtk, 2 * I), float("nan"), dtype=torch.bfloat16, device=DEV)
+    split(ic1, qx_t, xs_t, hs[0], hs[1], w13t, s13, None, top_k, 2, 2)
+    act_ref, q2, sq2 = ops.silu_mul_quant(ic1, write_act=True)
+    ic3 = torch.full((mtk, H), float("nan"), dtype=torch.bfloat16, device=DEV)
+    split(ic3, q2, sq2, hs[2], hs[3], w2t, s2w, tw, 1, 4, 1)
+    gpu_case(f"short-K pair I={I}: fused")
+    act = torch.full((mtk, I), float("nan"), dtype=torch.bfloat16, device=DEV)
+    y = torch.full((mtk, H), float("nan"), dtype=torch.bfloat16, device=DEV)
+    ops.moe_gemm_split_act(act, qx_t, xs_t, hs[0], hs[1], al[0:3], mtk, top_k, w13t, s13,
+                           al[3:6], sk=2)
+    ops.moe_gemm_split_qin(y, act, hs[2], hs[3], al[0:3], tw, mtk, w2t, s2w, al[3:6])
+    torch.cuda.synchronize()
+    assert not torch.isnan(y).any() and not torch.isnan(act).any()
+    assert torch.equal(act.view(torch.int16), act_ref.view(torch.int16))
+    assert torch.equal(y.view(torch.int16), ic3.view(torch.int16))
+
+
 def test_moe_gemm_split_act_qin_return_codes(pkg):
     """Size checks return before anything is launched (null operands included)."""
     P = ctypes.c_void_p
