@@ -136,9 +136,10 @@ __global__ __launch_bounds__(G * WAVE) void moe_gemm_k(
       auto pre = [&]() __attribute__((always_inline)) {   // the rows' loads, ahead of weights
         if (eid >= 0) {
 #pragma unroll
-          for (int p = 0; p < NP; ++p)
-            if (g0 + p * GS < ng)
-              raw[p] = *reinterpret_cast<const uint4*>(src + (g0 + p * GS) * 128);
+          for (int p = 0; p < NP; ++p)              // padding rows are zeros, not loaded
+            raw[p] = (ok && g0 + p * GS < ng)
+                         ? *reinterpret_cast<const uint4*>(src + (g0 + p * GS) * 128)
+                         : uint4{0u, 0u, 0u, 0u};
         }
       };
       auto pro = [&]() __attribute__((always_inline)) {
