@@ -41,9 +41,10 @@ __global__ __launch_bounds__(TB_THR) void tiles_k(const int* __restrict__ eids,
                                                   const int* __restrict__ npad, int nb_max,
                                                   int* __restrict__ tiles,
                                                   int* __restrict__ ntiles) {
+  constexpr int NW = TB_THR / WAVE;
   __shared__ int se[MAXNB];
-  __shared__ int part[TB_THR];
-  const int t = threadIdx.x;
+  __shared__ int wtot[2][NW];                       // per wave: max of run starts, tile count
+  const int t = threadIdx.x, lane = lane_id(), wv = t / WAVE;
   int nb = npad[0] >> 4;
   nb = nb < nb_max ? nb : nb_max;
   for (int b = t; b < nb; b += TB_THR) se[b] = eids[b];
@@ -55,31 +56,28 @@ __global__ __launch_bounds__(TB_THR) void tiles_k(const int* __restrict__ eids,
   int last = -1;
   for (int b = lo; b < hi; ++b)
     if (b == 0 || se[b] != se[b - 1]) last = b;
-  part[t] = last;
+  // the run start entering this thread's segment: an exclusive max-scan of the segments' last
+  // run starts, inside the wave by DPP and over the preceding waves' maxima
+  const int wmax = wave_incl_max(last);
+  if (lane == WAVE - 1) wtot[0][wv] = wmax;
   __syncthreads();
-  for (int d = 1; d < TB_THR; d <<= 1) {            // inclusive max-scan over the segments
-    const int v = t >= d ? part[t - d] : -1;
-    __syncthreads();
-    if (v > part[t]) part[t] = v;
-    __syncthreads();
-  }
-  const int carry = t > 0 ? part[t - 1] : -1;     // run start entering this segment
-  __syncthreads();
+  int pmax = -1;
+  for (int i = 0; i < wv; ++i) pmax = max(pmax, wtot[0][i]);
+  int carry = __shfl_up(max(wmax, pmax), 1);
+  if (lane == 0) carry = pmax;
   int rs = carry;
   int cnt = 0;
   for (int b = lo; b < hi; ++b) {
     if (b == 0 || se[b] != se[b - 1]) rs = b;
     cnt += se[b] >= 0 && (b - rs) % TMB == 0;
   }
-  part[t] = cnt;
+  // this thread's first tile index: an exclusive sum-scan of the tile counts, the same way
+  const int wsum = wave_incl_scan(cnt);
+  if (lane == WAVE - 1) wtot[1][wv] = wsum;
   __syncthreads();
-  for (int d = 1; d < TB_THR; d <<= 1) {            // inclusive sum-scan of the tile counts
-    const int v = t >= d ? part[t - d] : 0;
-    __syncthreads();
-    part[t] += v;
-    __syncthreads();
-  }
-  int pos = part[t] - cnt;
+  int psum = 0;
+  for (int i = 0; i < wv; ++i) psum += wtot[1][i];
+  int pos = psum + wsum - cnt;
   rs = carry;
   for (int b = lo; b < hi; ++b) {
     if (b == 0 || se[b] != se[b - 1]) rs = b;
@@ -91,7 +89,7 @@ __global__ __launch_bounds__(TB_THR) void tiles_k(const int* __restrict__ eids,
       ++pos;
     }
   }
-  if (t == TB_THR - 1) ntiles[0] = part[t];
+  if (t == TB_THR - 1) ntiles[0] = psum + wsum;
 }
 
 // ---- the tiled GEMM ------------------------------------------------------------------------

@@ -123,6 +123,17 @@ __device__ __forceinline__ int wave_incl_scan(int v) {
   return v;
 }
 
+// inclusive prefix max over the wave, for values >= -1 (lanes with no source take -1)
+__device__ __forceinline__ int wave_incl_max(int v) {
+  v = max(v, dpp<0x111>(-1, v));
+  v = max(v, dpp<0x112>(-1, v));
+  v = max(v, dpp<0x114>(-1, v));
+  v = max(v, dpp<0x118>(-1, v));
+  v = max(v, dpp<0x142, 0xa>(-1, v));
+  v = max(v, dpp<0x143, 0xc>(-1, v));
+  return v;
+}
+
 // Lanes of this wave holding the same `key` as this lane (all lanes call it; lanes with
 // valid == false match nothing and get 0). Bit-sliced: one ballot per key bit.
 __device__ __forceinline__ uint64_t match_any(int key, bool valid, int nbits) {

@@ -86,7 +86,11 @@ def test_group_quant_bitexact(ops, rows, K, group):
     assert np.array_equal(u8(q), q_w)
 
 
-@pytest.mark.parametrize("M,top_k,H", [(5, 10, 2560), (20, 10, 2560), (1, 1, 64), (3, 7, 1024)])
+# H 7168: two workgroups per row, the second partly idle; H 8: one lane; top_k 12: the
+# ten-row batch and then the tail rows one at a time
+@pytest.mark.parametrize("M,top_k,H", [(5, 10, 2560), (20, 10, 2560), (1, 1, 64), (3, 7, 1024),
+                                       (7, 10, 7168), (2, 3, 8), (9, 12, 2560),
+                                       (1024, 10, 2560)])
 def test_moe_sum_bitexact(ops, M, top_k, H):
     rng = np.random.default_rng(M * top_k)
     ic3 = fp8.bf16_round(rng.standard_normal((M * top_k, H)).astype(np.float32))
@@ -824,7 +828,11 @@ def tiles_ref(eids, npad, tmb=8):
     return out
 
 
-@pytest.mark.parametrize("M,E_used", [(256, 40), (600, 40), (37, 12)])
+# 4096 x 512: more blocks than threads (three per thread); 4096 x 10 and 12000 x 12: runs of
+# 256-750 blocks that cross many threads' segments and waves, the last one near the builder's
+# 8192-block limit
+@pytest.mark.parametrize("M,E_used", [(256, 40), (600, 40), (37, 12), (4096, 512), (4096, 10),
+                                      (12000, 12)])
 def test_moe_gemm_tile_list(ops, M, E_used):
     ids = routing(M, 10, E_used, seed=M)
     s, e, n = align_all(ids, E_used)
