@@ -174,15 +174,18 @@ __global__ __launch_bounds__(QT) void silu_mul_quant_g128_k(const uint16_t* __re
   }
 }
 
-// out [M, H] = sum over k of in [M * top_k + k, H]; grid (M, ceil(H / (QT*8)))
+// out [M, H] = sum over k of in [M * top_k + k, H]; one wave per 512 columns of a row, grid
+// (M, ceil(H / 512)): a decode call's few rows spread over as many CUs as the row has pieces
 // moe_sum rows loaded together: with top_k 10 all ten loads are in flight at once (the rows
 // are read in one memory round trip instead of ten, 3.82 -> 3.71 ms per 52-layer B=4 step)
 constexpr int SUMK = 10;
+constexpr int SUM_THR = WAVE;
 
-__global__ __launch_bounds__(QT) void moe_sum_k(const uint16_t* __restrict__ in, int top_k,
-                                                int H, uint16_t* __restrict__ out) {
+__global__ __launch_bounds__(SUM_THR) void moe_sum_k(const uint16_t* __restrict__ in,
+                                                     int top_k, int H,
+                                                     uint16_t* __restrict__ out) {
   const int m = blockIdx.x;
-  const int c = (blockIdx.y * QT + threadIdx.x) * 8;
+  const int c = (blockIdx.y * SUM_THR + threadIdx.x) * 8;
   if (c >= H) return;
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   const uint16_t* src = in + (size_t)m * top_k * H + c;
@@ -252,8 +255,9 @@ int rlu_silu_mul_quant(const void* x, int rows, int d, int ldx, int group, void*
 int rlu_moe_sum(const void* in, int M, int top_k, int H, void* out, hipStream_t stream) {
   if (M < 0 || top_k <= 0 || H <= 0 || H % 8) return -1;
   if (M == 0) return 0;
-  hipLaunchKernelGGL(rlu::moe_sum_k, dim3(M, (H + rlu::QT * 8 - 1) / (rlu::QT * 8)),
-                     dim3(rlu::QT), 0, stream, (const uint16_t*)in, top_k, H, (uint16_t*)out);
+  hipLaunchKernelGGL(rlu::moe_sum_k, dim3(M, (H + rlu::SUM_THR * 8 - 1) / (rlu::SUM_THR * 8)),
+                     dim3(rlu::SUM_THR), 0, stream, (const uint16_t*)in, top_k, H,
+                     (uint16_t*)out);
   return (int)hipGetLastError();
 }
 

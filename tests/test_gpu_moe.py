@@ -86,7 +86,7 @@ def test_group_quant_bitexact(ops, rows, K, group):
     assert np.array_equal(u8(q), q_w)
 
 
-# H 7168: two workgroups per row, the second partly idle; H 8: one lane; top_k 12: the
+# H 7168: 14 one-wave workgroups per row; H 8 and 64: one partly idle wave; top_k 12: the
 # ten-row batch and then the tail rows one at a time
 @pytest.mark.parametrize("M,top_k,H", [(5, 10, 2560), (20, 10, 2560), (1, 1, 64), (3, 7, 1024),
                                        (7, 10, 7168), (2, 3, 8), (9, 12, 2560),
