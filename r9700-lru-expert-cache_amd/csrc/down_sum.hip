@@ -3,15 +3,18 @@
 // the values rlu_moe_gemm_split (sk = 1) writes into ic3 followed by moe_sum_k, bit for bit,
 // without the [mtk, N] intermediate or the moe_sum launch.
 //
-// A workgroup owns one token and W x 16 output columns; wave w owns 16 of them and walks the
-// token's top_k experts in k order (top_k a compile-time constant: the loop is unrolled, so
-// the experts' addresses and routed weights sit in scalar registers, loaded up front). Per expert it runs the K steps of the grouped GEMM for the
+// A workgroup owns one token and W x 16 output columns. Each 16-column strip has KS waves, and
+// each of them walks its share of the token's top_k experts in k order (top_k a compile-time
+// constant: the loop is unrolled, so the experts' addresses and routed weights sit in scalar
+// registers, loaded up front). Per expert a wave runs the K steps of the grouped GEMM for the
 // token's A rows (one MFMA per step: 16 rows x 16 columns, of which row k is the one kept) with
-// the same per-step fma as moe_gemm_k, multiplies by the routed weight, rounds to bf16 and adds
-// the value into the running sum. The token's activation fragments for every K step are loaded
-// once and serve all top_k experts; the weights stream through a ring of NS stages (one
-// expert's K range) that runs on across experts, so expert k + 1's strip is in flight while
-// expert k is summed. Experts come from the layer's cache table: a resident expert from its
+// the same per-step fma as moe_gemm_k, multiplies by the routed weight and rounds to bf16; the
+// strip's values are then added in k order into one float32 sum. The token's activation
+// fragments for every K step are loaded once and serve all its experts; the weights stream
+// through a ring of NS stages (one expert's K range) that runs on across a wave's experts, so
+// expert k + 1's strip is in flight while expert k is summed. With the experts split over two
+// waves per strip (KSPLIT) a workgroup keeps twice the weight bytes in flight: the kernel is
+// bound by its loads' latency at these few tokens. Experts come from the layer's cache table: a resident expert from its
 // slot, any other from the full tensor (device or pinned host memory).
 //
 // Each expert strip is read once per token that routes to it; workgroups are laid out so that
@@ -32,24 +35,33 @@ constexpr int NXCD = 8;
 constexpr int BUF_WORD3 = 0x00020000;      // raw buffer descriptor word 3 on gfx9 (no format)
 constexpr int NTP = 2;                     // buffer cache policy: streaming
 constexpr int MAXK = 16;                   // top_k the kernel takes (A rows of one MFMA)
+constexpr int KSPLIT = 2;                  // waves per column strip (the experts split)
 
 // ACT: qa is the bf16 activation [M top_k, K] (the SiLU-mul output) and sa is not read; the
 // workgroup quantizes the token's rows per 128-column group into LDS first, exactly as
 // silu_mul_quant_g128_k does (same amax, scale and rounding), and the waves take their A
 // fragments and the rows' scales from there.
-template <int NS, int W, int TK, bool ACT = false>
-__global__ __launch_bounds__(W * WAVE) void down_sum_k(
+// KS: waves per column strip, each taking TK / KS of the token's experts (wave w % W owns the
+// strip, wave w / W the experts [(w / W) TK / KS, ...)). With KS > 1 the rounded per-expert
+// values go through LDS and the strip's first wave adds all TK of them in k order, so the sum
+// is the same; the point is twice the weight bytes in flight per workgroup.
+template <int NS, int W, int TK, bool ACT = false, int KS = 1>
+__global__ __launch_bounds__(W * KS * WAVE) void down_sum_k(
     const void* __restrict__ qa, const float* __restrict__ sa, const int* __restrict__ ids,
     const float* __restrict__ tw, const int* __restrict__ table,
     const uint8_t* __restrict__ hw, const float* __restrict__ hs,
     const uint8_t* __restrict__ cw, const float* __restrict__ cs,
     uint16_t* __restrict__ out, int M, int N, int E) {
   constexpr int K = NS * 128;
+  constexpr int TKH = TK / KS;                     // experts per wave
   static_assert(TK <= MAXK, "top_k rows fit one MFMA");
+  static_assert(TK % KS == 0, "experts split evenly over a strip's waves");
   constexpr int ALS = K + 16;                      // ACT: LDS row stride of the quantized rows
   __shared__ uint8_t alds[ACT ? TK * ALS : 16];
   __shared__ float xsl[ACT ? TK * NS : 4];
-  const int lane = lane_id(), w = uniform((int)(threadIdx.x / WAVE));
+  __shared__ float ys[KS > 1 ? TK * W * 16 : 1];  // KS > 1: [k][column] rounded values
+  const int lane = lane_id(), wi = uniform((int)(threadIdx.x / WAVE));
+  const int w = wi % W, kb = wi / W * TKH;        // column strip, first expert of this wave
   const int r16 = lane & 15, c4 = lane >> 4;
   // workgroup -> (token, column group): the tokens of one column group are consecutive within
   // an XCD's share of the grid (workgroup b runs on XCD b % 8)
@@ -60,19 +72,19 @@ __global__ __launch_bounds__(W * WAVE) void down_sum_k(
   const int cg = pos / M, t = pos - cg * M;
   const int col0 = (cg * W + w) * 16;
 
-  // the token's experts (scalar loads, all up front) and where each one's weights live
-  const uint8_t* wp[TK];
-  const float* sp[TK];
-  float twk[TK];
+  // this wave's experts kb + kk (scalar loads, all up front) and where their weights live
+  const uint8_t* wp[TKH];
+  const float* sp[TKH];
+  float twk[TKH];
 #pragma unroll
-  for (int k = 0; k < TK; ++k) {
-    int e = ids[t * TK + k];
+  for (int kk = 0; kk < TKH; ++kk) {
+    int e = ids[t * TK + kb + kk];
     e = e < 0 || e >= E ? 0 : e;
     const int s = table[e];
-    wp[k] = (s >= 0 ? hw + (size_t)s * N * K : cw + (size_t)e * N * K) + (size_t)col0 * K;
-    sp[k] = (s >= 0 ? hs + (size_t)s * (N / 128) * NS : cs + (size_t)e * (N / 128) * NS) +
-            (size_t)(col0 / 128) * NS;
-    twk[k] = tw[t * TK + k];
+    wp[kk] = (s >= 0 ? hw + (size_t)s * N * K : cw + (size_t)e * N * K) + (size_t)col0 * K;
+    sp[kk] = (s >= 0 ? hs + (size_t)s * (N / 128) * NS : cs + (size_t)e * (N / 128) * NS) +
+             (size_t)(col0 / 128) * NS;
+    twk[kk] = tw[t * TK + kb + kk];
   }
   // the token's A rows: row r16 of the MFMA is (t, k = r16); rows past top_k repeat row 0
   const int arow = t * TK + (r16 < TK ? r16 : 0);
@@ -93,22 +105,22 @@ __global__ __launch_bounds__(W * WAVE) void down_sum_k(
     rb[j][1] = __builtin_bit_cast(
         v4u, __builtin_amdgcn_raw_buffer_load_b128(b, voff + 1024, j * 2048, NTP));
   };
-  auto wbuf = [&](int k) __attribute__((always_inline)) {
-    return __builtin_amdgcn_make_buffer_rsrc((void*)wp[k < TK ? k : TK - 1], 0,
-                                             k < TK ? 16 * K : 0, BUF_WORD3);
+  auto wbuf = [&](int kk) __attribute__((always_inline)) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)wp[kk < TKH ? kk : TKH - 1], 0,
+                                             kk < TKH ? 16 * K : 0, BUF_WORD3);
   };
   // expert k's per-step scales (activation row (t, k) x weight block), vector loads issued one
   // expert ahead, so waiting for them waits only for weight loads already consumed
   float fx[2][NS], fw[2][NS];
-  auto load_scales = [&](int k, int q) __attribute__((always_inline)) {
-    const int kk = k < TK ? k : TK - 1;
+  auto load_scales = [&](int kk, int q) __attribute__((always_inline)) {
+    const int kq = kk < TKH ? kk : TKH - 1, r = kb + kq;
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
-      if constexpr (ACT)                           // row kk's scale, from LDS
-        fx[q][j] = xsl[kk * NS + j];
+      if constexpr (ACT)                           // row r's scale, from LDS
+        fx[q][j] = xsl[r * NS + j];
       else
-        fx[q][j] = sa[(size_t)(t * TK + kk) * NS + j];
-      fw[q][j] = sp[kk][j];
+        fx[q][j] = sa[(size_t)(t * TK + r) * NS + j];
+      fw[q][j] = sp[kq][j];
     }
   };
   // ACT: the workgroup quantizes the token's top_k rows into LDS once. The rows' loads go out
@@ -116,7 +128,7 @@ __global__ __launch_bounds__(W * WAVE) void down_sum_k(
   // order) does not wait for the weights: the quant runs while those are in flight. 16-lane
   // group q takes (row, 128-column group) pairs q, q + NG, ... and lane l16 columns
   // [8 l16, 8 l16 + 8) of each, as silu_mul_quant_g128_k does.
-  constexpr int NG = W * WAVE / 16, NPR = TK * NS, NPASS = (NPR + NG - 1) / NG;
+  constexpr int NG = W * KS * WAVE / 16, NPR = TK * NS, NPASS = (NPR + NG - 1) / NG;
   const int q16 = (int)threadIdx.x / 16, l16 = lane & 15;
   uint4 raw[ACT ? NPASS : 1];
   if constexpr (ACT) {
@@ -156,10 +168,10 @@ __global__ __launch_bounds__(W * WAVE) void down_sum_k(
   load_scales(0, 0);
   float sum = 0.f;
 #pragma unroll
-  for (int k = 0; k < TK; ++k) {
-    const int q = k & 1;
-    load_scales(k + 1, q ^ 1);
-    const __amdgpu_buffer_rsrc_t bn = wbuf(k + 1);
+  for (int kk = 0; kk < TKH; ++kk) {
+    const int q = kk & 1;
+    load_scales(kk + 1, q ^ 1);
+    const __amdgpu_buffer_rsrc_t bn = wbuf(kk + 1);
     v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
@@ -171,12 +183,27 @@ __global__ __launch_bounds__(W * WAVE) void down_sum_k(
       issue(j, bn);
       __builtin_amdgcn_sched_barrier(0);
     }
-    // row k sits in lanes c4 = k / 4, element k % 4: round it as the GEMM epilogue does, move
-    // it to the lanes of c4 = 0 and add it in k order
-    const float y = bf16_to_f32(f32_to_bf16(acc[k & 3] * twk[k]));
-    sum = __fadd_rn(sum, __shfl(y, r16 + 16 * (k >> 2)));
+    // row k sits in lanes c4 = k / 4, element k % 4: round it as the GEMM epilogue does, then
+    // add it in k order in the lanes of c4 = 0 (moved there, or through LDS with KS > 1)
+    if constexpr (KS == 1) {
+      const int k = kk;
+      const float y = bf16_to_f32(f32_to_bf16(acc[k & 3] * twk[kk]));
+      sum = __fadd_rn(sum, __shfl(y, r16 + 16 * (k >> 2)));
+    } else {
+      const int k = kb + kk, e4 = k & 3;          // wave-uniform
+      const float a = e4 == 0 ? acc[0] : e4 == 1 ? acc[1] : e4 == 2 ? acc[2] : acc[3];
+      const float y = bf16_to_f32(f32_to_bf16(a * twk[kk]));
+      if (c4 == (k >> 2)) ys[k * (W * 16) + w * 16 + r16] = y;
+    }
   }
-  if (c4 == 0) out[(size_t)t * N + col0 + r16] = f32_to_bf16(sum);
+  if constexpr (KS > 1) {
+    __syncthreads();
+    if (kb == 0 && c4 == 0) {
+#pragma unroll
+      for (int k = 0; k < TK; ++k) sum = __fadd_rn(sum, ys[k * (W * 16) + w * 16 + r16]);
+    }
+  }
+  if (kb == 0 && c4 == 0) out[(size_t)t * N + col0 + r16] = f32_to_bf16(sum);
 }
 
 }  // namespace dsum
@@ -198,9 +225,10 @@ int rlu_moe_down_sum(const void* q2, const float* s2, const int* topk_ids,
   if (K != 768 || top_k != 10) return -6;          // built for the 768-deep down, top-10
   if (N % 64) return -2;
   if (M == 0) return 0;
-  constexpr int W = 4;
+  constexpr int W = 4, KS = dsum::KSPLIT;
   const int grid = M * (N / (16 * W));
-  hipLaunchKernelGGL((dsum::down_sum_k<6, W, 10>), dim3(grid), dim3(W * WAVE), 0, stream, q2,
+  hipLaunchKernelGGL((dsum::down_sum_k<6, W, 10, false, KS>), dim3(grid), dim3(W * KS * WAVE), 0,
+                     stream, q2,
                      s2, topk_ids, topk_weights, table, (const uint8_t*)w_hot, s_hot,
                      (const uint8_t*)w_full, s_full, (uint16_t*)out, M, N, E);
   return (int)hipGetLastError();
@@ -220,10 +248,10 @@ int rlu_moe_down_sum_act(const void* act, const int* topk_ids, const float* topk
   if (K != 768 || top_k != 10) return -6;
   if (N % 64) return -2;
   if (M == 0) return 0;
-  constexpr int W = 4;
+  constexpr int W = 4, KS = dsum::KSPLIT;
   const int grid = M * (N / (16 * W));
-  hipLaunchKernelGGL((dsum::down_sum_k<6, W, 10, true>), dim3(grid), dim3(W * WAVE), 0, stream,
-                     act, nullptr, topk_ids, topk_weights, table, (const uint8_t*)w_hot, s_hot,
+  hipLaunchKernelGGL((dsum::down_sum_k<6, W, 10, true, KS>), dim3(grid), dim3(W * KS * WAVE), 0,
+                     stream, act, nullptr, topk_ids, topk_weights, table, (const uint8_t*)w_hot, s_hot,
                      (const uint8_t*)w_full, s_full, (uint16_t*)out, M, N, E);
   return (int)hipGetLastError();
 }
