@@ -670,6 +670,69 @@ def pcie_drift(torch, pkg, dev, rows=20, steps=400, window=50):
     return out
 
 
+def refill_slots(torch, pkg, layers):
+    """Every live slot <- the bytes of the expert its cache state names, copied from the pinned
+    pool by the library's own gather kernel with a miss list of every (expert, slot) pair. For
+    caches that were advanced without their gathers, and after capture(), whose eager step
+    gathers into slots and then puts the cache state back."""
+    for L in layers:
+        se = L.cache.slot_expert
+        live = torch.nonzero(se >= 0).flatten()
+        miss = torch.stack([se[live], live.to(torch.int32)], 1).contiguous()
+        n = torch.full((1,), miss.shape[0], dtype=torch.int32, device=se.device)
+        pairs = [(L.slots.w13, L.full.w13, L.full_ptrs[0]), (L.slots.w2, L.full.w2, L.full_ptrs[2]),
+                 (L.slots.s13, L.full.s13, L.full_ptrs[1]), (L.slots.s2, L.full.s2, L.full_ptrs[3])]
+        pairs += pairs[2:]
+        pkg._r4d_lru_gather([d for d, _, _ in pairs], [s_ for _, s_, _ in pairs], miss, n,
+                            pkg.lru.LRU_CHUNKS, pkg.lru.LRU_LANES,
+                            src_ptrs=[p_ for _, _, p_ in pairs])
+    torch.cuda.synchronize()
+
+
+def drift_e2e(torch, pkg, dev, host_full, slot_bufs, tw, hb, side, rows=20, steps=400,
+              window=50):
+    """The cache's benefit in time: the whole 52-layer step with the miss gather (overlapped)
+    over the last `window` steps of the 400-step drifting traces, LRU against the static arm.
+    Each arm's caches start from the layers' warm sets and are advanced through the first
+    steps - window steps of routing by the fused LRU kernel alone (the state those steps
+    leave is what matters; their gathers would only move bytes that later steps evict), then
+    every slot is refilled with its expert's bytes over the host link, and the last `window`
+    steps replay the captured step graph: gather, GEMMs over slots and over pinned host memory,
+    moe_sum. -> {arm: ms per step}, plus the window's host-link bytes per step."""
+    trace = pkg.traces
+    ids = np.empty((steps, LAYERS, rows, TOPK), np.int32)
+    warm = []
+    for l in range(LAYERS):
+        tr, perm0 = layer_trace(l, rows, steps)
+        ids[:, l] = tr.reshape(steps, rows, TOPK)
+        warm.append(trace.warm_hot(perm0, S))
+    ids_dev = torch.from_numpy(ids).to(dev)
+    ids_static = torch.empty_like(ids_dev[0])
+    t0 = steps - window
+    out = {}
+    for arm, mi in (("lru", None), ("static", 0)):
+        layers = build_from(torch, pkg, rows, warm, dev, None, host_full, slot_bufs,
+                            max_inserts=mi)
+        for t in range(t0):
+            for l, L in enumerate(layers):
+                L.cache.fused(ids_dev[t, l], out=L.align)
+        torch.cuda.synchronize()
+        ids_static.copy_(ids_dev[t0])
+        g = capture(torch, layers, ids_static, tw, hb, gather=True, side=side)
+        refill_slots(torch, pkg, layers)
+        ms, _ = time_steps(torch, g, ids_dev, ids_static, t0, window - PCIE_STEPS)
+        pc = pcie_per_step(torch, layers, g, ids_dev, ids_static, steps - PCIE_STEPS,
+                           PCIE_STEPS)
+        out[arm] = {"e2e_with_gather_ms_per_step": round(ms, 3), "pcie_mb_per_step": pc[0],
+                    "inserted_per_layer": pc[1], "cold_per_layer": pc[2]}
+        log(f"drifted end, {arm} arm: {ms:.3f} ms/step, {pc[0]} MB/step over PCIe")
+        del g, layers
+        torch.cuda.synchronize()
+    out["steps"], out["timed"] = steps, f"steps {t0}..{steps - PCIE_STEPS - 1} timed, " \
+        f"{steps - PCIE_STEPS}..{steps - 1} replayed one at a time to count host-link bytes"
+    return out
+
+
 def profile_routing(pkg, rows, steps):
     """Routing that follows the reference's hot profile (tests/golden/hot_profile.json: 48 MoE
     layers of routing counts from real decode and prefill traffic): layer l of the 52 draws
@@ -1050,7 +1113,7 @@ def main():
         torch.cuda.synchronize()
         # B=1: the same slot buffers, refilled with the B=1 warm-start sets; fresh caches
         rows1 = 5
-        layers1, ids1 = build(torch, pkg, rows1, args.warmup + 2 * args.steps + 2, dev, pool,
+        layers1, ids1 = build(torch, pkg, rows1, args.warmup + 3 * args.steps + 2, dev, pool,
                               host_full, layers_cache=layers4)
         tw1 = torch.softmax(torch.randn(rows1, TOPK, generator=g), -1).to(dev)
         hb1 = torch.empty((LAYERS + 1, rows1, H), dtype=torch.bfloat16, device=dev)
@@ -1081,7 +1144,18 @@ def main():
         out["b1_misses_per_layer_last_step"] = round(
             float(np.mean([int(L.cache.n_miss.item()) for L in layers1])), 2)
         log(f"B=1 with PCIe miss gather: {ms1e:.3f} ms")
-        del g1e, layers1
+        del g1e
+        torch.cuda.synchronize()
+        # the same steps from the same point with the gather in front of the GEMMs, where the
+        # layer folds down and moe_sum into one kernel (the fold runs only without the overlap)
+        refill_slots(torch, pkg, layers1)
+        g1f = capture(torch, layers1, ids1_static, tw1, hb1, gather=True, side=side,
+                      overlap=False)
+        refill_slots(torch, pkg, layers1)
+        ms1f, _ = time_steps(torch, g1f, ids1_dev, ids1_static, t1 + 1 + args.steps, args.steps)
+        out["b1_e2e_no_overlap_folded_ms_per_step"] = round(ms1f, 3)
+        log(f"B=1 with PCIe miss gather, not overlapped, down + moe_sum folded: {ms1f:.3f} ms")
+        del g1f, layers1
         torch.cuda.synchronize()
         # B=4, HBM-resident, on the uncorrelated trace (about twice the distinct experts)
         layersU, idsU = build(torch, pkg, rows4, args.warmup + args.steps + 2, dev, pool,
@@ -1145,6 +1219,8 @@ def main():
             f"{out['pcie_drift']['lru']['mb_last']} MB/step, static "
             f"{out['pcie_drift']['static']['mb_first']} -> "
             f"{out['pcie_drift']['static']['mb_last']}")
+        out["drift_e2e"] = drift_e2e(torch, pkg, dev, host_full, [L.slots for L in layers4],
+                                     tw4, hb4, side)
         out["lm_head_fp8"] = lm_head_fp8(torch, pkg, dev)
         log(f"fp8 lm_head M=5: {out['lm_head_fp8']['us']} us")
         out["lm_head_w4"] = lm_head_w4(torch, pkg, dev)

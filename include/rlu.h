@@ -234,8 +234,8 @@ int rlu_moe_gemm_fp8blk_tiled_silu_quant(const void* qx, const float* xs, const 
  * [M, top_k] (every id in [0, E)); table int32 [E] (expert -> slot or -1, the cache state after
  * this step's manager); expert e comes from slot table[e] of w_hot / s_hot when resident, else
  * from w_full / s_full (device or pinned host memory), both in fragment order with 128x128
- * block scales. Built for K = 768 and top_k = 10 (-6 otherwise); N % 64 == 0. Returns -1 / -2 /
- * -6 or a HIP error code. */
+ * block scales. Every pointer is required (NULL returns -1). Built for K = 768 and top_k = 10
+ * (-6 otherwise); N % 128 == 0 (-2 otherwise). Returns -1 / -2 / -6 or a HIP error code. */
 int rlu_moe_down_sum(const void* q2, const float* s2, const int* topk_ids,
                      const float* topk_weights, const int* table, const void* w_hot,
                      const float* s_hot, const void* w_full, const float* s_full, void* out,

@@ -11,7 +11,7 @@ Modules:
   clru    ctypes binding of lru_oracle.c: an independent serial (argmin-per-insert) C
           restatement of the same functions, used to pin the numpy one
   fp8     bit-exact float32 <-> OCP e4m3fn conversion and the block / group / SiLU quantizers
-  gemm    fp32-dequant grouped MoE GEMM, moe_sum and the dense lm_head reference
+  gemm    fp32-dequant grouped MoE GEMM and moe_sum
   w4      the int4 group-128 quantizer, this build's W4 layout, and the float64 W4 GEMV
 
 Parity status of every function is listed in each module's header.

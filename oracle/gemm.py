@@ -10,8 +10,6 @@
   moe_sum()    out[m] = bf16(sum_k in[m * top_k + k]) in float32, k ascending (the contract of
                vLLM's moe_sum as used at r4d_mxfp4_moe.py.lru.diff:696; its own accumulation
                order is parity unpinned -- vLLM is absent -- this is the build's convention).
-  dense()      y = dequant(qx, xs) @ dequant(w, ws)^T, float64 (kernels/fp8_target_lmhead.py
-               :70-74 and the fp32 oracle recipe of tests/k3/test_fp8sk.py:37-43,77).
 """
 from __future__ import annotations
 
@@ -56,12 +54,6 @@ def moe_sum(ic3: np.ndarray, M: int, top_k: int) -> np.ndarray:
     for k in range(top_k):
         acc = np.float32(acc + x[:, k])
     return fp8.bf16_round(acc)
-
-
-def dense(qx, xs, w, ws) -> np.ndarray:
-    A = fp8.dequant_act(qx, xs).astype(np.float64)
-    W = fp8.dequant_weight(w, ws).astype(np.float64)
-    return A @ W.T
 
 
 def rel_err(got, want) -> float:

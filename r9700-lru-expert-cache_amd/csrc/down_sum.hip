@@ -219,11 +219,11 @@ int rlu_moe_down_sum(const void* q2, const float* s2, const int* topk_ids,
                      int M, int top_k, int K, int N, int E, hipStream_t stream) {
   using namespace rlu;
   if (M < 0 || top_k < 1 || top_k > dsum::MAXK || K <= 0 || N <= 0 || E <= 0) return -1;
-  if (!q2 || !s2 || !topk_ids || !topk_weights || !table || !w_full || !s_full || !out)
+  if (!q2 || !s2 || !topk_ids || !topk_weights || !table || !w_hot || !s_hot || !w_full ||
+      !s_full || !out)
     return -1;
-  if (K % 128 || N % 128) return -2;
+  if (K % 128 || N % 128) return -2;               // 128x128 weight blocks
   if (K != 768 || top_k != 10) return -6;          // built for the 768-deep down, top-10
-  if (N % 64) return -2;
   if (M == 0) return 0;
   constexpr int W = 4, KS = dsum::KSPLIT;
   const int grid = M * (N / (16 * W));
@@ -243,10 +243,11 @@ int rlu_moe_down_sum_act(const void* act, const int* topk_ids, const float* topk
                          int K, int N, int E, hipStream_t stream) {
   using namespace rlu;
   if (M < 0 || top_k < 1 || top_k > dsum::MAXK || K <= 0 || N <= 0 || E <= 0) return -1;
-  if (!act || !topk_ids || !topk_weights || !table || !w_full || !s_full || !out) return -1;
+  if (!act || !topk_ids || !topk_weights || !table || !w_hot || !s_hot || !w_full || !s_full ||
+      !out)
+    return -1;
   if (K % 128 || N % 128) return -2;
   if (K != 768 || top_k != 10) return -6;
-  if (N % 64) return -2;
   if (M == 0) return 0;
   constexpr int W = 4, KS = dsum::KSPLIT;
   const int grid = M * (N / (16 * W));

@@ -26,7 +26,7 @@ from .lru import LRU_CHUNKS, LRU_LANES, LruCache, _r4d_lru_gather, split_fresh
 _P = ctypes.c_void_p
 BLOCK = 16
 # Routed rows (tokens x top_k) from which a layer runs the tiled (prefill) grouped GEMM instead
-# of the decode one: a 2048-token chunk at top-10 gives 20480, ~40 rows per expert over 512.
+# of the decode one: 2048 rows are about 205 tokens at top-10, about 4 rows per expert over 512.
 PREFILL_ROWS = 2048
 # Tokens up to which a decode step folds moe_sum into the down projection (ops.moe_down_sum):
 # the token-major kernel reads each expert strip once per token routed to it, which pays at

@@ -399,8 +399,9 @@ def moe_gemm_tiled_noalloc(y: torch.Tensor, qx: torch.Tensor, x_scale: torch.Ten
         raise ValueError(f"moe_gemm_tiled_noalloc: {nb} blocks exceed the scratch tile list "
                          f"({NOALLOC_MAX_BLOCKS} blocks)")
     rc = lib().rlu_moe_gemm_fp8blk_tiled_noalloc(
-        _p(qx), _p(x_scale), _p(wq), _p(ws_t), _p(sorted_ids), _p(expert_ids), _p(num_post_pad),
-        nb, _p(topk_weights), _p(y), mtk, top_k, K, N, wv, _P(stream_ptr()))
+        _p(qx), _p(x_scale), _P(device_ptr(wq)), _P(device_ptr(ws_t)), _p(sorted_ids),
+        _p(expert_ids), _p(num_post_pad), nb, _p(topk_weights), _p(y), mtk, top_k, K, N, wv,
+        _P(stream_ptr()))
     check(rc, "rlu_moe_gemm_fp8blk_tiled_noalloc")
 
 

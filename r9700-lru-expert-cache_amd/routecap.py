@@ -23,9 +23,11 @@ Env (defaults as the reference's):
 from __future__ import annotations
 
 import ctypes
+import io
 import os
+import tempfile
 import threading
-import time
+import warnings
 
 import numpy as np
 import torch
@@ -39,14 +41,14 @@ OUT_DIR = os.environ.get("ROUTECAP_DIR", ".")
 
 
 def _rank() -> int:
-    """routecap.py:103-116: the torch.distributed rank, else the launcher's, else the device."""
-    import torch.distributed as dist
+    """The N of routes_rank<N>.npz (the precedence of routecap.py:103-116): a live process
+    group names it; failing that, the launcher's variables in the order VLLM_WORKER_RANK, RANK,
+    LOCAL_RANK; failing those, the current device index."""
+    dist = torch.distributed
     if dist.is_available() and dist.is_initialized():
         return dist.get_rank()
-    for v in ("VLLM_WORKER_RANK", "RANK", "LOCAL_RANK"):
-        if os.environ.get(v):
-            return int(os.environ[v])
-    return torch.cuda.current_device()
+    set_vars = [name for name in ("VLLM_WORKER_RANK", "RANK", "LOCAL_RANK") if os.environ.get(name)]
+    return int(os.environ[set_vars[0]]) if set_vars else torch.cuda.current_device()
 
 
 def complete_slots(steps: np.ndarray, ctr: int, high: int) -> list[int]:
@@ -82,12 +84,19 @@ class RouteRing:
                                    device=self.dev)
         self.ring_step = torch.full((ring,), -1, dtype=torch.int64, device=self.dev)
         self.dump_stream = torch.cuda.Stream(device=self.dev)
+        # host mirrors of the ring, pinned once here so that a poll allocates nothing and its
+        # copies run asynchronously on the dump stream
+        self._h_ctr = torch.empty(1, dtype=torch.int64, pin_memory=True)
+        self._h_step = torch.empty(ring, dtype=torch.int64, pin_memory=True)
+        self._h_ids = torch.empty((nlayer, ring, self.width), dtype=torch.int16, pin_memory=True)
+        self._copied = torch.cuda.Event()
         self.saved_steps: list[int] = []
         self.saved_ids: list[np.ndarray] = []
         self.high = -1          # the highest step already saved
         self.dumps = 0
         self._lock = threading.Lock()
         self._thread = None
+        self._stop = threading.Event()
 
     # -- device side ------------------------------------------------------------------------
     def capture(self, layer: int, topk_ids: torch.Tensor) -> None:
@@ -116,19 +125,25 @@ class RouteRing:
 
     # -- host side --------------------------------------------------------------------------
     def poll(self) -> int:
-        """Copy the ring to the host on the dump stream and keep every newly completed slot:
-        a slot is complete once a later step has started (its step number is below the
-        counter); the newest one may still be being written. Returns the counter read."""
+        """Bring the ring to the host and append every slot that completed since the last poll.
+        The counter is copied first, then the step numbers and ids, all on the dump stream, so
+        a slot whose step is below the copied counter was finished before its copy began (the
+        capture of a later step has started); the slot of the counter's own step may be half
+        written and waits for the next poll. Returns the counter."""
         with torch.cuda.stream(self.dump_stream):
-            ctr = int(self.ctr.item())
-            steps = self.ring_step.to("cpu", copy=True).numpy()
-            ring = self.ring_ids.to("cpu", copy=True).numpy()
-        self.dump_stream.synchronize()
+            self._h_ctr.copy_(self.ctr, non_blocking=True)
+            self._h_step.copy_(self.ring_step, non_blocking=True)
+            self._h_ids.copy_(self.ring_ids, non_blocking=True)
+            self._copied.record(self.dump_stream)
+        self._copied.synchronize()
+        ctr = int(self._h_ctr[0])
+        steps = self._h_step.numpy()
         with self._lock:
-            for s in complete_slots(steps, ctr, self.high):
-                self.saved_steps.append(int(steps[s]))
-                self.saved_ids.append(ring[:, s, :].copy())
-                self.high = int(steps[s])
+            keep = complete_slots(steps, ctr, self.high)
+            if keep:
+                self.saved_steps.extend(int(steps[s]) for s in keep)
+                self.saved_ids.extend(self._h_ids.numpy()[:, keep, :].transpose(1, 0, 2))
+                self.high = self.saved_steps[-1]
             self.dumps += 1
         return ctr
 
@@ -150,34 +165,57 @@ class RouteRing:
                     lost_to_wrap=np.int64(self.lost_to_wrap()))
 
     def flush(self, out_dir: str | None = None, rank: int | None = None) -> dict:
-        """routecap.py:119-152: poll, then rewrite routes_rank<rank>.npz atomically (a temporary
-        file renamed over the old one)."""
+        """Poll, then replace routes_rank<rank>.npz (routecap.py:119-152) so that a reader
+        never sees a partial file: the archive is built in memory, written to a fresh file
+        beside the target and renamed over it."""
         ctr = self.poll()
-        out_dir = OUT_DIR if out_dir is None else out_dir
-        os.makedirs(out_dir, exist_ok=True)
-        p = os.path.join(out_dir, f"routes_rank{_rank() if rank is None else rank}.npz")
-        tmp = p + ".tmp"
+        target_dir = OUT_DIR if out_dir is None else out_dir
+        os.makedirs(target_dir, exist_ok=True)
+        rank = _rank() if rank is None else rank
+        path = os.path.join(target_dir, f"routes_rank{rank}.npz")
         r = self.routes(ctr)
-        with open(tmp, "wb") as fh:        # a bare path would get ".npz" appended
-            np.savez(fh, **r)
-        os.replace(tmp, p)
-        return dict(path=p, ctr=ctr, saved=int(r["steps"].size),
+        blob = io.BytesIO()
+        np.savez(blob, **r)
+        fd, staged = tempfile.mkstemp(prefix=f".routes_rank{rank}.", dir=target_dir)
+        try:
+            with os.fdopen(fd, "wb") as fh:
+                fh.write(blob.getbuffer())
+            os.replace(staged, path)
+        except BaseException:
+            if os.path.exists(staged):
+                os.unlink(staged)
+            raise
+        return dict(path=path, ctr=ctr, saved=int(r["steps"].size),
                     lost_to_wrap=int(r["lost_to_wrap"]))
 
     def start_dumper(self, every_s: float = DUMP_S, out_dir: str | None = None):
-        """routecap.py:155-161: a daemon thread that flushes every every_s seconds."""
-        def loop():
+        """A daemon thread that flushes every every_s seconds until stop_dumper()
+        (routecap.py:155-161). A failed flush is reported as a warning and the next period
+        tries again."""
+        if self._thread is not None:
+            return self._thread
+
+        def run():
             torch.cuda.set_device(self.dev)
-            while True:
-                time.sleep(every_s)
+            while not self._stop.wait(every_s):
                 try:
                     self.flush(out_dir)
                 except Exception as exc:                            # noqa: BLE001
-                    print(f"[routecap] flush failed: {type(exc).__name__}: {exc}", flush=True)
-        if self._thread is None:
-            self._thread = threading.Thread(target=loop, daemon=True, name="routecap")
-            self._thread.start()
+                    warnings.warn(f"routecap flush to {out_dir or OUT_DIR!r} failed: {exc!r}")
+
+        self._stop.clear()
+        self._thread = threading.Thread(target=run, daemon=True, name="routecap-dumper")
+        self._thread.start()
         return self._thread
+
+    def stop_dumper(self, flush: bool = True, out_dir: str | None = None) -> None:
+        """Stop the dumper thread (if any) and, by default, write one last flush."""
+        if self._thread is not None:
+            self._stop.set()
+            self._thread.join()
+            self._thread = None
+        if flush:
+            self.flush(out_dir)
 
     def status(self) -> dict:
         """routecap.py:189-197 (routecap_status)."""

@@ -35,3 +35,25 @@ def pkg():
 def gpu_case(msg: str) -> None:
     """Name the case before each GPU step, flushed, so a fault still says what ran."""
     print(f"[gpu-case] {msg}", flush=True)
+
+
+def check_argmax(got, ref, what: str, max_ties: int = 1) -> int:
+    """Per-row argmax of a kernel's logits against the reference's. A row may pick another
+    index only when that index is in the reference's top two and the two reference logits lie
+    within one bf16 step (2^-7 relative) of each other; each such row is printed, and at most
+    max_ties rows of one call may take that branch. Returns the number of such rows."""
+    import numpy as np
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    am, ar = got.argmax(1), ref.argmax(1)
+    ties = []
+    for r in np.nonzero(am != ar)[0]:
+        top2 = np.argpartition(ref[r], -2)[-2:]
+        assert am[r] in top2, f"{what}: row {r} argmax {am[r]} not in the reference top two {top2}"
+        gap = ref[r, ar[r]] - ref[r, am[r]]
+        assert gap <= 2 ** -7 * abs(ref[r, ar[r]]), f"{what}: row {r} gap {gap:.3e}"
+        ties.append((int(r), int(am[r]), int(ar[r]), float(gap)))
+    if ties:
+        print(f"[argmax] {what}: near-tie rows (row, got, ref, gap) {ties}", flush=True)
+    assert len(ties) <= max_ties, f"{what}: {len(ties)} near-tie rows > {max_ties}"
+    return len(ties)

@@ -145,10 +145,23 @@ def test_one_layer_e512_s257_softmax_gates(pkg, pool):
             if name != "routed":
                 assert np.array_equal(got.cpu().numpy(), getattr(st, name)), (t, name)
         inserted += int(st.n_miss[0])
+        if st.n_miss[0] > 0:
+            fresh = int(st.miss[0, 1])              # a slot this step installed
         audit_slots(layer, pool, f"C2 step {t}")
         err = ogemm.rel_err(out.float().cpu().numpy(), oracle_layer(x, ids, tw, pool))
         assert err <= TOL, f"step {t}: rel err {err:.3e}"
     assert inserted > 0, "the steps must install experts"
+    # negative control (tests/lru/test_slots_prod.py:162-169): one flipped byte of a slot the
+    # gather just filled, in each of the four buffers, must fail the audit; restored, it passes
+    for attr in ("w13", "s13", "w2", "s2"):
+        flat = getattr(layer.slots, attr)[fresh].view(torch.uint8).reshape(-1)
+        off = flat.numel() // 2 + 3
+        flip = torch.full((1,), 0x5A, dtype=torch.uint8, device=DEV)
+        flat[off:off + 1].bitwise_xor_(flip)
+        with pytest.raises(AssertionError):
+            audit_slots(layer, pool, f"C2 flipped {attr}")
+        flat[off:off + 1].bitwise_xor_(flip)
+        audit_slots(layer, pool, f"C2 restored {attr}")
 
 
 def test_52_layer_b4_graph_replays(pkg, pool):

@@ -4,6 +4,8 @@ The capture hook of LruMoELayer is exercised inside a captured layer step in
 test_gpu_layer.py::test_layer_overlap_graph_replay."""
 from __future__ import annotations
 
+import time
+
 import numpy as np
 import pytest
 
@@ -142,3 +144,25 @@ def test_capture_in_a_graph_polls_and_writes_the_file(rc, tmp_path):
     assert int(back["maxrows"]) == maxrows and int(back["ctr"]) == 43
     assert back["ids"].dtype == np.int16 and back["ids"].shape == (37, L, maxrows * k)
     assert int(back["lost_to_wrap"]) == 5
+
+
+def test_dumper_thread_flushes_and_stops(rc, tmp_path):
+    """The background dumper writes routes_rank<N>.npz on its own while steps run, and
+    stop_dumper ends the thread and writes a last flush holding every finished step."""
+    L, k, rows = 2, 10, 3
+    r = rc.RouteRing(L, k, DEV, ring=64, maxrows=4)
+    rng = np.random.default_rng(7)
+    gpu_case("routecap dumper thread")
+    r.start_dumper(every_s=0.02, out_dir=str(tmp_path))
+    for _ in range(20):
+        for li in range(L):
+            r.capture(li, torch.from_numpy(rng.integers(0, 512, (rows, k)).astype(np.int32))
+                      .to(DEV))
+        torch.cuda.synchronize()
+        time.sleep(0.005)
+    r.stop_dumper(out_dir=str(tmp_path))
+    assert r._thread is None and r.dumps >= 2
+    files = sorted(p.name for p in tmp_path.iterdir())
+    assert files == [f"routes_rank{rc._rank()}.npz"], files    # no staging file left behind
+    back = rc.load_routes(tmp_path / files[0])
+    assert list(back["steps"]) == list(range(1, 20)) and int(back["ctr"]) == 20

@@ -4,6 +4,9 @@ library's per-device scratch array -- called through the C-ABI, equals the exist
 calls in a row, the second with a smaller input (fewer tokens, so fewer tiles than the first
 call left in the scratch); gate_up without and down with routed weights; outputs poisoned
 with NaN so an unwritten or stale row shows. Sizes past the scratch are refused unlaunched.
+The Python wrapper passes pinned host weights by their device-visible address, and a gate_up +
+down pair captured into a HIP graph reuses the scratch correctly over replays with new routing
+and fewer live tokens.
 """
 from __future__ import annotations
 
@@ -91,3 +94,94 @@ def test_noalloc_refuses_past_the_scratch(pkg, weights):
     with pytest.raises(ValueError, match="scratch"):
         pkg.ops.moe_gemm_tiled_noalloc(y, q, s_, w13, s13, small, torch.zeros(
             8193, dtype=torch.int32, device=DEV), small, None, 16, TOPK)
+
+
+def test_noalloc_pinned_weights_through_the_wrapper(pkg, weights):
+    """ops.moe_gemm_tiled_noalloc passes the device-visible address of pinned host weights (the
+    cold call's full expert tensor), as moe_gemm_tiled does: both equal bit for bit."""
+    _, _, w2, s2 = weights
+    ops = pkg.ops
+    hw = torch.empty(w2.shape, dtype=w2.dtype, pin_memory=True)
+    hw.copy_(w2)
+    hs = torch.empty(s2.shape, dtype=s2.dtype, pin_memory=True)
+    hs.copy_(s2)
+    T = 48
+    rng = np.random.default_rng(5)
+    ids = np.stack([rng.choice(E, TOPK, replace=False) for _ in range(T)]).astype(np.int32)
+    mtk = ids.size
+    cache = pkg.LruCache.build(E, range(E), None, DEV)
+    (sh, eh, nh), _ = cache.fused(torch.from_numpy(ids).to(DEV), out=cache.alloc_align(mtk))
+    g = torch.Generator(device=DEV).manual_seed(6)
+    _, q2, sc2 = ops.silu_mul_quant(torch.randn(mtk, 2 * I, device=DEV, generator=g)
+                                    .to(torch.bfloat16))
+    tw = torch.rand(mtk, device=DEV, generator=g)
+    want = torch.full((mtk, H), float("nan"), dtype=torch.bfloat16, device=DEV)
+    got = torch.full_like(want, float("nan"))
+    gpu_case("noalloc pinned weights: workspace entry")
+    ops.moe_gemm_tiled(want, q2, sc2, hw, hs, sh, eh, nh, tw, mtk, 1)
+    gpu_case("noalloc pinned weights: scratch entry")
+    ops.moe_gemm_tiled_noalloc(got, q2, sc2, hw, hs, sh, eh, nh, tw, mtk, 1)
+    torch.cuda.synchronize()
+    assert not torch.isnan(want).any()
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+def test_noalloc_pair_replayed_in_a_graph(pkg, weights):
+    """What the entry is for: after one eager call (which looks up the scratch address), the
+    fused align and a gate_up + down pair of no-alloc calls are captured into one HIP graph and
+    replayed with new routing, some replays with fewer live tokens (the other rows' ids -1, so
+    fewer blocks and tiles than the scratch last held). Eager work and synchronizations run
+    between the replays; after each, both outputs equal the workspace entry run eagerly on that
+    replay's align output, bit for bit (rows the align does not name stay NaN in both)."""
+    w13, s13, w2, s2 = weights
+    ops = pkg.ops
+    T = 512
+    mtk = T * TOPK
+    cache = pkg.LruCache.build(E, range(E), None, DEV)
+    al = cache.alloc_align(mtk)
+    ids_dev = torch.empty((T, TOPK), dtype=torch.int32, device=DEV)
+    g = torch.Generator(device=DEV).manual_seed(77)
+    qx, xs = ops.fp8_quant_group(torch.randn(T, H, device=DEV, generator=g).to(torch.bfloat16))
+    _, q2, sc2 = ops.silu_mul_quant(torch.randn(mtk, 2 * I, device=DEV, generator=g)
+                                    .to(torch.bfloat16))
+    tw = torch.rand(mtk, device=DEV, generator=g)
+    y1 = torch.empty((mtk, 2 * I), dtype=torch.bfloat16, device=DEV)
+    y2 = torch.empty((mtk, H), dtype=torch.bfloat16, device=DEV)
+
+    def routing(seed, live):
+        rng = np.random.default_rng(seed)
+        ids = np.stack([rng.choice(E, TOPK, replace=False) for _ in range(T)]).astype(np.int32)
+        ids[live:] = -1
+        return torch.from_numpy(ids)
+
+    def body():
+        cache.fused(ids_dev, out=al)
+        ops.moe_gemm_tiled_noalloc(y1, qx, xs, w13, s13, al[0], al[1], al[2], None, mtk, TOPK)
+        ops.moe_gemm_tiled_noalloc(y2, q2, sc2, w2, s2, al[0], al[1], al[2], tw, mtk, 1)
+
+    ids_dev.copy_(routing(0, T))
+    gpu_case("noalloc graph: eager first call")
+    body()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    gpu_case("noalloc graph: capture")
+    with torch.cuda.graph(graph):
+        body()
+    torch.cuda.synchronize()
+    for rep, live in enumerate((T, 200, T, 37)):
+        ids_dev.copy_(routing(rep + 1, live))
+        y1.fill_(float("nan"))
+        y2.fill_(float("nan"))
+        gpu_case(f"noalloc graph: replay {rep} with {live} live tokens")
+        graph.replay()
+        torch.cuda.synchronize()
+        r1 = torch.full_like(y1, float("nan"))
+        r2 = torch.full_like(y2, float("nan"))
+        ops.moe_gemm_tiled(r1, qx, xs, w13, s13, al[0], al[1], al[2], None, mtk, TOPK)
+        ops.moe_gemm_tiled(r2, q2, sc2, w2, s2, al[0], al[1], al[2], tw, mtk, 1)
+        torch.cuda.synchronize()
+        assert not torch.isnan(r1[:live * TOPK]).any() and not torch.isnan(r2[:live * TOPK]).any()
+        if live < T:
+            assert torch.isnan(r2[live * TOPK:]).all()
+        assert torch.equal(y1.view(torch.int16), r1.view(torch.int16)), (rep, live)
+        assert torch.equal(y2.view(torch.int16), r2.view(torch.int16)), (rep, live)
