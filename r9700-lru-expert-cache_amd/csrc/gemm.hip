@@ -77,8 +77,16 @@ __global__ __launch_bounds__(G * WAVE) void moe_gemm_k(
   const int r16 = lane & 15;
   int parity = 0;
 
-  for (int grp = blockIdx.x; grp < ngroups; grp += gridDim.x, parity ^= 1) {
-    const int item = grp * IPG + sub;
+  // MODE 2 takes its item groups in an XCD-aware order. Workgroup g runs on XCD g % 8 (the
+  // dispatcher deals workgroups round-robin over the 8 XCDs), so XCD x gets the contiguous run
+  // [x per, (x + 1) per) of the groups: the ten groups of one block then share one L2, which
+  // fetches the block's activation rows once instead of once per XCD (the launch rounds its
+  // grid up to a multiple of 8 workgroups; indices past ngroups are dead).
+  const int per = (ngroups + 7) >> 3;
+  const int nloop = AL ? 8 * per : ngroups;
+  for (int grp = blockIdx.x; grp < nloop; grp += gridDim.x, parity ^= 1) {
+    const int lg = AL ? (grp & 7) * per + (grp >> 3) : grp;
+    const int item = lg * IPG + sub;
     bool live = item < nitems;
     int b = live ? item / ntiles : 0;
     const int n0 = live ? (item - b * ntiles) * NT : 0;
@@ -402,7 +410,7 @@ int rlu_moe_gemm_split_qin(const void* act, const void* wq_hot, const float* ws_
   const int nb = (em + 15) / 16;
   const int nblive = nsets * nb < mtk ? nsets * nb : mtk;
   const int items = nblive * (N / 64);
-  const int grid = (items + rlu::QIN_G - 1) / rlu::QIN_G;
+  const int grid = ((items + rlu::QIN_G - 1) / rlu::QIN_G + 7) / 8 * 8;   // XCD-aware order
   const rlu::WSet s0{(const uint8_t*)wq_hot, ws_hot, sorted_hot, eids_hot, npad_hot};
   const rlu::WSet s1{(const uint8_t*)wq, ws, sorted_cold, eids_cold, npad_cold};
   return rlu::launch<false, 2>(4, 1, grid, stream, (const uint8_t*)act, nullptr, s0,

@@ -26,12 +26,35 @@ __device__ __forceinline__ float scale_of(uint32_t amax_bits) {
   return s > MIN_SCALE ? s : MIN_SCALE;
 }
 
-// quantize 8 values with one scale -> 8 e4m3 bytes
+// a / s rounded to nearest, for s >= MIN_SCALE, without a division per value: with r =
+// RN(1 / s), q0 = RN(a r) is within an ulp or two of a / s, e = a - q0 s is exact (one FMA),
+// and RN(q0 + e r) is the correctly rounded quotient (Markstein's correction; P. Markstein,
+// IBM J. Res. Dev. 34(1), 1990). It carries the sign of a, as the quotient does (the FMA turns
+// -0 + +0 into +0). Where the correction cannot apply, the uncorrected q0 gives the same e4m3
+// code: |q0| >= 448 (the clamp decides; that covers q0 = Inf), and an infinite s (an infinite
+// amax), where q0 = a * 0 is what the division gives. Every kernel here quantizes bf16 values
+// with a scale made from their bf16 amax; that whole input space, both signs, is checked
+// against IEEE division code for code by the GPU tests.
+struct RecipScale {
+  float s, r;
+  bool fin;
+  __device__ __forceinline__ explicit RecipScale(float s_)
+      : s(s_), r(__fdiv_rn(1.0f, s_)), fin(s_ < __builtin_inff()) {}
+  __device__ __forceinline__ float quot(float a) const {
+    const float q0 = __fmul_rn(a, r);
+    const float e = __fmaf_rn(-q0, s, a);
+    const float q1 = __builtin_copysignf(__fmaf_rn(e, r, q0), a);
+    return (fin && fabsf(q0) < E4M3_MAX) ? q1 : q0;
+  }
+};
+
+// quantize 8 values with one scale -> 8 e4m3 bytes: e4m3(clamp(a / s, +-448)), nearest even
 __device__ __forceinline__ uint2 quant8(const float (&a)[8], float s) {
+  const RecipScale rs(s);
   uint32_t w[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    float x0 = __fdiv_rn(a[2 * j], s), x1 = __fdiv_rn(a[2 * j + 1], s);
+    float x0 = rs.quot(a[2 * j]), x1 = rs.quot(a[2 * j + 1]);
     x0 = fminf(fmaxf(x0, -E4M3_MAX), E4M3_MAX);
     x1 = fminf(fmaxf(x1, -E4M3_MAX), E4M3_MAX);
     w[j] = f32x2_to_e4m3(x0, x1);
