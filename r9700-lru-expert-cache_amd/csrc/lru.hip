@@ -5,7 +5,7 @@
 // lru_fused_k :418-575, lru_gather_k :271-301); the entry points at the bottom keep its C-ABI.
 // The implementation is this build's own, shaped for wave64 CDNA4:
 //
-//  * One workgroup of 256 threads (one wave per SIMD), seven barriers for the fused kernel at
+//  * One workgroup of 256 threads (one wave per SIMD), six barriers for the fused kernel at
 //    decode sizes (three for the manager). Every global load is issued up front, so the kernel
 //    pays one memory round trip, not one per phase. Decode-sized align outputs are built in
 //    LDS and written once, coalesced, with the sentinels past num_post_pad written directly;
@@ -65,6 +65,10 @@ struct LruLds {
                                      // base of the token chunk being placed
   int vslot[MAXINS];                 // victim slot of rank r
   int vold[MAXINS];                  // expert evicted from it (or -1)
+  int vrank[MAXS];                   // align: the rank of the miss a slot takes this step, or -1
+  int vcnt[MAXINS];                  // align: tokens of the miss of rank r < nact
+  int vexp[MAXINS];                  // align: the miss of rank r < nins (ascending expert id)
+  int mpw[NW][NWORD];                // align: each wave's own copy of the miss prefix (mpre)
   uint64_t vkey[MAXINS];             // victims, compacted, before ranking
   int vpack[MAXINS];                 // (slot << 16) | (old expert & 0xffff), same order
   int cnt_h[MAXS];                   // post-update tokens per hot bucket (slot)
@@ -125,6 +129,7 @@ __device__ __forceinline__ bool bit_of(const uint64_t* bm, int e) {
 __device__ __forceinline__ void put_victim(LruLds& L, int p, int slot, int old) {
   L.vslot[p] = slot;
   L.vold[p] = old;
+  L.vrank[slot] = p;
 }
 
 // rank the n compacted keys L.vkey[0..n) among themselves (keys unique), then install
@@ -417,6 +422,36 @@ __device__ __forceinline__ int post_slot(const LruLds& L, int e, int S, int nact
   return -1;
 }
 
+// The step's install count as any wave can derive it from the routed, non-resident and
+// busy-slot bitmaps -- the number wave 0's victim search arrives at: nins = the misses (in
+// ascending expert id) up to max_inserts, none on a read-through step (more than max_distinct
+// experts routed); nact = min(nins, evictable slots). Also writes this wave's copy of the
+// per-bitmap-word miss prefix (mp[w] = misses in words below w).
+struct InsCount {
+  int nins, nact;
+};
+__device__ __forceinline__ InsCount insert_counts(const LruLds& L, int S, int max_distinct,
+                                                  int max_inserts, int* mp) {
+  const int lane = lane_id();
+  uint64_t rw = 0, nw = 0, sb = 0;
+  if (lane < NWORD) {
+    rw = L.rbits[lane];
+    nw = L.nres[lane];
+    sb = L.sbusy[lane];
+  }
+  const int distinct = readlane(row_sum(__popcll(rw)), 0);          // words live in row 0
+  const int busy = readlane(row_sum(__popcll(sb)), 0);
+  const int mpop = __popcll(rw & nw);
+  const int mincl = row_incl_scan(mpop);
+  const int total = readlane(mincl, NWORD - 1);
+  if (lane < NWORD) mp[lane] = mincl - mpop;
+  InsCount r;
+  r.nins = distinct <= max_distinct ? (total < max_inserts ? total : max_inserts) : 0;
+  const int nev = S - busy;
+  r.nact = r.nins < nev ? r.nins : nev;
+  return r;
+}
+
 // The per-token-group-128 quant of the layer's hidden state, run by workgroups 1.. of the fused
 // launch while workgroup 0 runs the cache: the two are independent and both feed the first
 // GEMM, so one launch serves both. One row per wave: the launch's LDS footprint leaves room for
@@ -489,7 +524,10 @@ __global__ __launch_bounds__(NT) void lru_k(
       fill_align(sorted_hot, sorted_cold, eids_hot, eids_cold, defer_place ? 0 : Lsz, NB, mk,
                  vec_out);
     }
-    for (int i = t; i < S; i += NT) L.cnt_h[i] = 0;
+    for (int i = t; i < S; i += NT) {
+      L.cnt_h[i] = 0;
+      L.vrank[i] = -1;
+    }
   }
 #pragma unroll
   for (int j = 0; j < EJ; ++j) {
@@ -593,6 +631,12 @@ __global__ __launch_bounds__(NT) void lru_k(
   } else {
     const uint64_t rw = lane < NWORD ? L.rbits[lane] : 0ull;
     const bool ins_ok = readlane(row_sum(__popcll(rw)), 0) <= max_distinct;
+    // with the align, the misses' buckets too: how many misses get a slot follows from the
+    // bitmaps alone (wave 0's search only decides which slots), so a miss of rank < nact
+    // leaves its token count for the slot it takes (vcnt) and the others go cold
+    const InsCount ic = ALIGN ? insert_counts(L, S, max_distinct, max_inserts, L.mpw[w])
+                              : InsCount{0, 0};
+    if (ALIGN) wave_lds_sync();
     if (ins_ok) {                                    // hit: r4d_lru.hip:228-238
       for (int i = t - WAVE; i < S; i += NT - WAVE)
         if (bit_of(L.sbusy, i)) slot_stamp[i] = st;
@@ -601,11 +645,19 @@ __global__ __launch_bounds__(NT) void lru_k(
       const bool r = bit_of(L.rbits, e);
       routed[e] = r ? 1 : 0;
       const int s0 = L.tab[e];
-      if (ALIGN && !(r && s0 < 0)) {
+      if (ALIGN) {
         const int c = r ? expert_tokens(L, e, staged) : 0;
-        const bool hot = r && (unsigned)s0 < (unsigned)S;
-        if (hot) L.cnt_h[s0] = c;
-        L.cnt_c[e] = (r && !hot) ? c : 0;
+        if (r && s0 < 0) {
+          const uint64_t mw = L.rbits[e >> 6] & L.nres[e >> 6];
+          const int rank = L.mpw[w][e >> 6] + __popcll(mw & ((1ull << (e & 63)) - 1ull));
+          if (rank < ic.nins) L.vexp[rank] = e;
+          if (rank < ic.nact) L.vcnt[rank] = c;
+          L.cnt_c[e] = rank < ic.nact ? 0 : c;
+        } else {
+          const bool hot = r && (unsigned)s0 < (unsigned)S;
+          if (hot) L.cnt_h[s0] = c;
+          L.cnt_c[e] = (r && !hot) ? c : 0;
+        }
         L.ecnt[e] = 0;  // general path: becomes the running per-expert base of the chunks
       }
     }
@@ -615,38 +667,35 @@ __global__ __launch_bounds__(NT) void lru_k(
   const int nact = L.misc[0];
   const int nins = L.misc[1];
 
-  // ---- misses: miss list, installs, post-update bucket counts ------------------------------
-#pragma unroll
-  for (int j = 0; j < EJ; ++j) {
-    const int e = t + NT * j;
-    if (e >= E) continue;
-    if (!(tab[j] < 0 && bit_of(L.rbits, e))) continue;
-    int post = -1;
-    if (nins > 0) {
-      const uint64_t mw = L.rbits[e >> 6] & L.nres[e >> 6];
-      const int rank = L.mpre[e >> 6] + __popcll(mw & ((1ull << (e & 63)) - 1ull));
-      if (rank < nins) miss[2 * rank] = e;
-      if (rank < nact) {
-        const int sl = L.vslot[rank];
-        const int old = L.vold[rank];
-        if (old >= 0 && old < E) {
-          table[old] = -1;
-          map_cold[old] = old;
-        }
-        table[e] = sl;
-        map_cold[e] = -1;
-        slot_expert[sl] = e;
-        slot_stamp[sl] = st;
-        miss[2 * rank + 1] = sl;
-        post = sl;
+  // ---- misses: miss list and installs (global stores only: every bucket count is in LDS
+  // already, so the scans below start without another barrier). With the align the misses come
+  // by rank from vexp (one thread per rank); without it each thread checks its experts ------
+  auto install = [&](int rank, int e) __attribute__((always_inline)) {
+    if (rank < nins) miss[2 * rank] = e;
+    if (rank < nact) {
+      const int sl = L.vslot[rank];
+      const int old = L.vold[rank];
+      if (old >= 0 && old < E) {
+        table[old] = -1;
+        map_cold[old] = old;
       }
+      table[e] = sl;
+      map_cold[e] = -1;
+      slot_expert[sl] = e;
+      slot_stamp[sl] = st;
+      miss[2 * rank + 1] = sl;
     }
-    if (ALIGN) {
-      const int c = expert_tokens(L, e, staged);
-      const bool hot = (unsigned)post < (unsigned)S;
-      if (hot) L.cnt_h[post] = c;
-      L.cnt_c[e] = hot ? 0 : c;
-      L.ecnt[e] = 0;
+  };
+  if (ALIGN) {
+    for (int r = t; r < nins; r += NT) install(r, L.vexp[r]);
+  } else {
+#pragma unroll
+    for (int j = 0; j < EJ; ++j) {
+      const int e = t + NT * j;
+      if (e >= E) continue;
+      if (!(tab[j] < 0 && bit_of(L.rbits, e)) || nins == 0) continue;
+      const uint64_t mw = L.rbits[e >> 6] & L.nres[e >> 6];
+      install(L.mpre[e >> 6] + __popcll(mw & ((1ull << (e & 63)) - 1ull)), e);
     }
   }
   if (t == 0) {
@@ -654,8 +703,6 @@ __global__ __launch_bounds__(NT) void lru_k(
     n_miss[0] = nact;
   }
   if (!ALIGN) return;
-
-  lds_barrier();  // 4
 
   // ---- block-padded exclusive scans: thread t owns a contiguous run of slots and experts ---
   const Blk B(BSC ? BSC : bs);
@@ -665,7 +712,13 @@ __global__ __launch_bounds__(NT) void lru_k(
   int ph[EJ], pc[EJ], a = 0, b = 0;
 #pragma unroll
   for (int j = 0; j < EJ; ++j) {
-    ph[j] = (j < Ch && h0 + j < h1) ? L.cnt_h[h0 + j] : 0;
+    // a slot's bucket: its resident expert's tokens, or those of the miss installed in it
+    int hv = 0;
+    if (j < Ch && h0 + j < h1) {
+      const int vr = L.vrank[h0 + j];
+      hv = L.cnt_h[h0 + j] + (vr >= 0 ? L.vcnt[vr] : 0);
+    }
+    ph[j] = hv;
     pc[j] = (j < Ce && c0 + j < c1) ? L.cnt_c[c0 + j] : 0;
     a += B.pad(ph[j]);
     b += B.pad(pc[j]);
@@ -675,7 +728,7 @@ __global__ __launch_bounds__(NT) void lru_k(
     L.wsum[w][0] = ai;
     L.wsum[w][1] = bi;
   }
-  lds_barrier();  // 5
+  lds_barrier();  // 4
   int runa = ai - a, runb = bi - b, tota = 0, totb = 0;
 #pragma unroll
   for (int x = 0; x < NW; ++x) {
@@ -702,7 +755,7 @@ __global__ __launch_bounds__(NT) void lru_k(
   } else
     place_buckets(L, sorted_hot, sorted_cold, eids_hot, eids_cold, ph, pc, h0, h1, c0, c1, runa,
                   runb, NB, B, -1);
-  lds_barrier();  // 6
+  lds_barrier();  // 5
 
   if (staged) {
     // ---- each token places itself: its bucket's start plus the number of the bucket's tokens
@@ -723,7 +776,7 @@ __global__ __launch_bounds__(NT) void lru_k(
           L.stage_c[pos] = t;
       }
     }
-    lds_barrier();  // 7
+    lds_barrier();  // 6
     // ---- copy the staged outputs out, coalesced; past num_post_pad the sentinels ------------
     const int nbh = B.blk(tota), nbc = B.blk(totb);
     int k0 = 0;
