@@ -69,7 +69,8 @@ struct LruLds {
   int vcnt[MAXINS];                  // align: tokens of the miss of rank r < nact
   int vexp[MAXINS];                  // align: the miss of rank r < nins (ascending expert id)
   int mpw[NW][NWORD];                // align: each wave's own copy of the miss prefix (mpre)
-  uint64_t vkey[MAXINS];             // victims, compacted, before ranking
+  alignas(16) uint64_t vkey[MAXINS]; // victims, compacted, before ranking
+  alignas(16) int hist[256];         // the victim search's digit histogram
   int vpack[MAXINS];                 // (slot << 16) | (old expert & 0xffff), same order
   int cnt_h[MAXS];                   // post-update tokens per hot bucket (slot)
   int cnt_c[MAXE];                   // post-update tokens per cold bucket (expert)
@@ -135,7 +136,8 @@ __device__ __forceinline__ void put_victim(LruLds& L, int p, int slot, int old) 
 // rank the n compacted keys L.vkey[0..n) among themselves (keys unique), then install
 __device__ __forceinline__ void rank_compacted(LruLds& L, int n) {
   wave_lds_sync();
-  for (int p = lane_id(); p < n; p += WAVE) {
+  const int lane = lane_id();
+  for (int p = lane; p < n; p += WAVE) {
     const uint64_t v = L.vkey[p];
     int r = 0;
     int j = 0;
@@ -208,36 +210,48 @@ __device__ __forceinline__ int select_victims(LruLds& L, int S, int nins, const 
       }
       return nact;
     }
-    // boundary stamp: tau = largest rel with #{rel < tau} < nact (two bits per round)
+    // boundary stamp: tau = the nact-th smallest rel (#{rel < tau} < nact <= #{rel <= tau}),
+    // found 8 bits at a time from the top of the range: each pass counts, in an LDS histogram,
+    // the next digit of the slots whose higher digits equal tau's so far, and one wave scan
+    // over the 256 bins finds the bin where the running count reaches nact
     uint32_t rel[Q];
 #pragma unroll
     for (int q = 0; q < Q; ++q) rel[q] = ev[q] ? (uint32_t)sst[q] - mn : ~0u;
-    int b = 32 - __clz(mx - mn);                    // mx > mn here: cnt0 < nact <= nev
+    const int b = 32 - __clz(mx - mn);              // mx > mn here: cnt0 < nact <= nev
     uint32_t tau = 0;
-    if (b & 1) {
-      --b;
-      const uint32_t c1 = tau | (1u << b);
-      int n1 = 0;
+    int clt = 0;                                    // #{rel < tau's prefix so far}
+    for (int sh = ((b - 1) >> 3) << 3; sh >= 0; sh -= 8) {
+      *reinterpret_cast<int4*>(&L.hist[4 * lane]) = make_int4(0, 0, 0, 0);
+      wave_lds_sync();
+      const bool top = sh + 8 >= 32;
+      const uint32_t pre = top ? 0u : tau >> (sh + 8);
 #pragma unroll
-      for (int q = 0; q < Q; ++q) n1 += __popcll(__ballot(rel[q] < c1));
-      if (n1 < nact) tau = c1;
-    }
-    while (b > 0) {
-      b -= 2;
-      const uint32_t u = 1u << b;
-      const uint32_t c1 = tau + u, c2 = tau + 2 * u, c3 = tau + 3 * u;
-      int n1 = 0, n2 = 0, n3 = 0;
-#pragma unroll
-      for (int q = 0; q < Q; ++q) {
-        n1 += __popcll(__ballot(rel[q] < c1));
-        n2 += __popcll(__ballot(rel[q] < c2));
-        n3 += __popcll(__ballot(rel[q] < c3));
+      for (int q = 0; q < Q; ++q)
+        if (ev[q] && (top || (rel[q] >> (sh + 8)) == pre))
+          atomicAdd(&L.hist[(rel[q] >> sh) & 255u], 1);
+      wave_lds_sync();
+      const int4 h = *reinterpret_cast<const int4*>(&L.hist[4 * lane]);
+      const int sum = h.x + h.y + h.z + h.w;
+      const int c0 = clt + wave_incl_scan(sum) - sum;   // counted before this lane's bins
+      const int c1 = c0 + h.x, c2 = c1 + h.y, c3 = c2 + h.z, c4 = c3 + h.w;
+      int d = -1, cb = 0;
+      if (c0 < nact && nact <= c1) {
+        d = 0;
+        cb = c0;
+      } else if (c1 < nact && nact <= c2) {
+        d = 1;
+        cb = c1;
+      } else if (c2 < nact && nact <= c3) {
+        d = 2;
+        cb = c2;
+      } else if (c3 < nact && nact <= c4) {
+        d = 3;
+        cb = c3;
       }
-      tau += (uint32_t)((n1 < nact) + (n2 < nact) + (n3 < nact)) * u;
+      const int ln = __ffsll((unsigned long long)__ballot(d >= 0)) - 1;   // exactly one lane
+      tau |= (uint32_t)(4 * ln + readlane(d, ln)) << sh;
+      clt = readlane(cb, ln);
     }
-    int clt = 0;
-#pragma unroll
-    for (int q = 0; q < Q; ++q) clt += __popcll(__ballot(rel[q] < tau));
     const int need = nact - clt;                    // >= 1 taken from the tau group
     bool vic[Q];
     uint64_t key[Q];
