@@ -29,7 +29,7 @@ of 8 TB/s. `lru_fused_us_per_layer` is the fused LRU kernel (manager + both alig
 launched eagerly). `prefill_4096` times the prefill kernels on a 4096-token chunk; `cpu_baseline` the
 layer step in torch fp32 on the host cores.
 
-    python bench.py [--steps K] [--warmup W] [--only-b4]
+    python bench.py [--steps K] [--warmup W] [--only-b4 | --only-b1]
 """
 from __future__ import annotations
 
@@ -560,11 +560,35 @@ def lru_insert_sweep(torch, pkg, dev, reps=50, rounds=5):
     return out
 
 
+def down_sum_probe(torch, pkg, dev, calls=20, M=5):
+    """The B=1 folded down + moe_sum kernel from the activation (rlu_moe_down_sum_act) at the
+    decode shape, for the counter runs: w2 e4m3 [512, 2560, 768] with 128x128 block scales, 257
+    of the experts resident in slots, M tokens of top-10 (each token's ten experts distinct,
+    half of them resident), `calls` calls."""
+    g = torch.Generator(device=dev).manual_seed(11)
+    w2 = _fp8_bytes(torch, (E, H, I), dev, g)
+    s2 = torch.rand((E, H // 128, I // 128), device=dev, generator=g) * 1e-3 + 1e-4
+    hot = torch.randperm(E, device=dev, generator=g)[:S].sort().values
+    table = torch.full((E,), -1, dtype=torch.int32, device=dev)
+    table[hot] = torch.arange(S, dtype=torch.int32, device=dev)
+    w_hot, s_hot = w2[hot].contiguous(), s2[hot].contiguous()
+    ids = torch.stack([torch.randperm(E, device=dev, generator=g)[:TOPK] for _ in range(M)])
+    ids = ids.to(torch.int32).contiguous()
+    tw = torch.rand((M, TOPK), device=dev, generator=g)
+    act = torch.randn((M * TOPK, I), device=dev, generator=g).to(torch.bfloat16)
+    out = torch.empty((M, H), dtype=torch.bfloat16, device=dev)
+    for _ in range(calls):
+        pkg.ops.moe_down_sum_act(act, ids, tw, table, w_hot, s_hot, w2, s2, out)
+    torch.cuda.synchronize()
+    del w2, w_hot
+
+
 def counter_probe(torch, pkg, dev, calls=50):
     """The workload of the LDS and MFMA counter runs: the fused LRU kernel in the insert storm
     (E=512, S=257, mk 200 with no read-through; `calls` calls with 0 inserts, then `calls` with
     64, each from the same pristine state, restored by copies between the calls), then the
-    prefill grouped GEMMs (gate_up and down, 4 launches each)."""
+    prefill grouped GEMMs (gate_up, down, SiLU-mul-quant and the fused gate_up, 4 launches
+    each), then the B=1 folded down + moe_sum (20 calls), then the 256 MiB calibration copy."""
     for k in (0, 64):
         rng = np.random.default_rng(100 + k)
         hot = np.sort(rng.choice(E, S, replace=False))
@@ -581,6 +605,7 @@ def counter_probe(torch, pkg, dev, calls=50):
         torch.cuda.synchronize()
         assert int(cache.n_miss.item()) == k
     res = prefill_gemm(torch, pkg, dev, reps=3, lru=False)
+    down_sum_probe(torch, pkg, dev)
     # the calibration kernel of known size for FETCH_SIZE / WRITE_SIZE: a 256 MiB device copy,
     # the run's last copy dispatch
     a = torch.ones(256 << 20, dtype=torch.uint8, device=dev)
@@ -591,7 +616,8 @@ def counter_probe(torch, pkg, dev, calls=50):
     print(json.dumps({"counter_probe": f"lru_k: {calls} calls at 0 inserts, then {calls} at 64 "
                                        "(mk 200); then the prefill kernels (4096 tokens): "
                                        "gate_up, down, SiLU-mul-quant, fused gate_up x4 each; "
-                                       "then one 256 MiB device-to-device copy",
+                                       "then the B=1 folded down + moe_sum from the activation "
+                                       "x20; then one 256 MiB device-to-device copy",
                       "copy_bytes": 256 << 20, "prefill": res}), flush=True)
 
 
@@ -668,6 +694,32 @@ def pcie_drift(torch, pkg, dev, rows=20, steps=400, window=50):
     out["routing"] = ("the headline's layer traces (seed 1000 + layer, rows correlated), "
                       f"{steps} steps; per-layer means over the first and last {window}")
     return out
+
+
+def b1_leg(torch, pkg, dev, pool, host_full, layers4, hb4, side, g, args):
+    """The B=1 (5 tokens) HBM-resident 52-layer step on the B=4 layers' slot buffers, refilled
+    with the B=1 warm-start sets (fresh caches): the step's ms and its GEMM roofline."""
+    rows1 = 5
+    layers1, ids1 = build(torch, pkg, rows1, args.warmup + 3 * args.steps + 2, dev, pool,
+                          host_full, layers_cache=layers4)
+    tw1 = torch.softmax(torch.randn(rows1, TOPK, generator=g), -1).to(dev)
+    hb1 = torch.empty((LAYERS + 1, rows1, H), dtype=torch.bfloat16, device=dev)
+    hb1[0] = hb4[0, :rows1]
+    ids1_dev = torch.from_numpy(ids1).to(dev)
+    ids1_static = torch.empty_like(ids1_dev[0])
+    ids1_static.copy_(ids1_dev[0])
+    g1 = capture(torch, layers1, ids1_static, tw1, hb1, gather=False, side=side)
+    run_steps(torch, g1, ids1_dev, ids1_static, 0, args.warmup)
+    ms1, _ = time_steps(torch, g1, ids1_dev, ids1_static, args.warmup, args.steps)
+    log(f"B=1 HBM-resident step: {ms1:.3f} ms")
+    r1 = gemm_roofline(torch, pkg, layers1, ids1[args.warmup + args.steps - 1], rows1)
+    roof = {k: r1[k] for k in ("bound", "achieved", "peak", "unit", "frac", "kernel",
+                               "avg_launch_us", "algorithmic_bytes_per_launch",
+                               "distinct_experts_per_layer")}
+    log(f"B=1 grouped GEMM: {roof['achieved']} GB/s, frac {roof['frac']}")
+    del g1
+    return {"b1_ms_per_step": round(ms1, 4), "b1_roofline": roof,
+            "state": (layers1, ids1, tw1, hb1, ids1_dev, ids1_static)}
 
 
 def refill_slots(torch, pkg, layers):
@@ -968,6 +1020,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--only-b4", action="store_true",
                     help="only the B=4 HBM-resident step (the profiled command)")
+    ap.add_argument("--only-b1", action="store_true",
+                    help="only the B=1 HBM-resident step (its profiled command); prints the B=1 "
+                         "figures instead of the bench line")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--counter-probe", action="store_true",
                     help="for LDS / MFMA counter runs: the fused LRU kernel in the insert storm "
@@ -1031,6 +1086,11 @@ def main():
                           "copy_bytes": 256 << 20, "gemm_launches": 2 * LAYERS,
                           "algorithmic_bytes_per_launch": int(per),
                           "distinct_experts_per_layer": round(float(d.mean()), 2)}), flush=True)
+        return
+    if args.only_b1:
+        b1 = b1_leg(torch, pkg, dev, pool, host_full, layers4, hb4, side, g, args)
+        print(json.dumps({"only_b1": True, "b1_ms_per_step": b1["b1_ms_per_step"],
+                          "b1_roofline": b1["b1_roofline"]}), flush=True)
         return
     gB = capture(torch, layers4, ids4_static, tw4, hb4, gather=False, side=side)
     log(f"setup {time.perf_counter() - t_setup:.1f}s; warmup {args.warmup} steps")
@@ -1113,27 +1173,10 @@ def main():
         torch.cuda.synchronize()
         # B=1: the same slot buffers, refilled with the B=1 warm-start sets; fresh caches
         rows1 = 5
-        layers1, ids1 = build(torch, pkg, rows1, args.warmup + 3 * args.steps + 2, dev, pool,
-                              host_full, layers_cache=layers4)
-        tw1 = torch.softmax(torch.randn(rows1, TOPK, generator=g), -1).to(dev)
-        hb1 = torch.empty((LAYERS + 1, rows1, H), dtype=torch.bfloat16, device=dev)
-        hb1[0] = hb4[0, :rows1]
-        ids1_dev = torch.from_numpy(ids1).to(dev)
-        ids1_static = torch.empty_like(ids1_dev[0])
-        ids1_static.copy_(ids1_dev[0])
-        g1 = capture(torch, layers1, ids1_static, tw1, hb1, gather=False, side=side)
-        run_steps(torch, g1, ids1_dev, ids1_static, 0, args.warmup)
-        ms1, _ = time_steps(torch, g1, ids1_dev, ids1_static, args.warmup, args.steps)
-        out["b1_ms_per_step"] = round(ms1, 4)
-        log(f"B=1 HBM-resident step: {ms1:.3f} ms")
-        r1 = gemm_roofline(torch, pkg, layers1, ids1[args.warmup + args.steps - 1], rows1)
-        out["b1_roofline"] = {k: r1[k] for k in ("bound", "achieved", "peak", "unit", "frac",
-                                                  "kernel", "avg_launch_us",
-                                                  "algorithmic_bytes_per_launch",
-                                                  "distinct_experts_per_layer")}
-        log(f"B=1 grouped GEMM: {out['b1_roofline']['achieved']} GB/s, frac "
-            f"{out['b1_roofline']['frac']}")
-        del g1
+        b1 = b1_leg(torch, pkg, dev, pool, host_full, layers4, hb4, side, g, args)
+        layers1, ids1, tw1, hb1, ids1_dev, ids1_static = b1["state"]
+        out["b1_ms_per_step"] = b1["b1_ms_per_step"]
+        out["b1_roofline"] = b1["b1_roofline"]
         torch.cuda.synchronize()
         # the same B=1 steps with the miss gather (overlapped) in the graph
         t1 = args.warmup + args.steps
