@@ -25,9 +25,17 @@ from .lru import LRU_CHUNKS, LRU_LANES, LruCache, _r4d_lru_gather, split_fresh
 
 _P = ctypes.c_void_p
 BLOCK = 16
-# Routed rows (tokens x top_k) from which a layer runs the tiled (prefill) grouped GEMM instead
-# of the decode one: 2048 rows are about 205 tokens at top-10, about 4 rows per expert over 512.
-PREFILL_ROWS = 2048
+# Routed rows per expert (tokens x top_k / E) from which a layer runs the prefill grouped GEMMs
+# instead of the decode one. Measured crossover of the whole layer step at E = 512, top-10,
+# every expert resident, graph-replayed (us, decode / prefill kernels):
+#   tokens (rows per expert)   Zipf(1.1) routing   uniform routing
+#   256 (5.0)                  429 / 464           508 / 530
+#   320 (6.25)                 500 / 482           527 / 514
+#   512 (10)                   613 / 546           548 / 553
+#   1024 (20)                  852 / 648           856 / 582
+# The decode kernel reads an expert's weights once per 16-row block, the prefill kernels once
+# per tile of up to 128 rows, behind a fixed cost of their own (tile list, persistent grid).
+PREFILL_ROWS_PER_EXPERT = 6
 # Tokens up to which a decode step folds moe_sum into the down projection (ops.moe_down_sum):
 # the token-major kernel reads each expert strip once per token routed to it, which pays at
 # B=1 (5 tokens: 16.3 vs 18.9 us per layer for down + moe_sum) and loses at B=4 (20 tokens:
@@ -62,7 +70,7 @@ class LruMoELayer:
                  top_k: int, device="cuda", slots: ExpertWeights | None = None,
                  npw1: int = 2, npw2: int = 4, sk1: int | None = None, sk2: int = 1,
                  wv: int = 0, max_inserts: int | None = None,
-                 prefill_rows: int = PREFILL_ROWS, fold_sum: bool | None = None,
+                 prefill_rows: int | None = None, fold_sum: bool | None = None,
                  fuse_act: bool | None = None):
         """npw / sk: 16-column tiles per item and K split of gate_up (1) and down (2); the
         defaults are the fastest measured at the decode shapes (hidden 2560, intermediate
@@ -77,7 +85,8 @@ class LruMoELayer:
         prefill_rows: from this many routed rows (max_tokens x top_k) on, both GEMMs run the
         tiled prefill kernel (ops.moe_gemm_tiled: whole expert tiles, the weights streamed
         once per tile) over the hot and the cold align, in place of the decode kernel; npw /
-        sk / wv do not apply to it. Its output equals the decode kernel's with sk = 1 bit
+        sk / wv do not apply to it. Default PREFILL_ROWS_PER_EXPERT x E (3072 rows, about
+        307 tokens at top-10, over 512 experts). Its output equals the decode kernel's with sk = 1 bit
         for bit. The reference runs prefill chunks through the same split path
         (r4d_mxfp4_moe.py.lru.diff:659-696; tests/lru/test_numerics_prod.py:44-48).
 
@@ -129,6 +138,8 @@ class LruMoELayer:
         self.route_capture = None
         self.qx = torch.empty((self.M, self.H), dtype=ops.FP8, device=dev)
         self.xs = torch.empty((self.M, self.H // 128), dtype=torch.float32, device=dev)
+        if prefill_rows is None:
+            prefill_rows = PREFILL_ROWS_PER_EXPERT * self.E
         self.prefill = self.mtk >= prefill_rows
         if fold_sum is None:
             # not for the static arm: its cold experts are the common case, and the folded
