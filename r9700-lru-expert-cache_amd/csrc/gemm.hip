@@ -65,8 +65,11 @@ __global__ __launch_bounds__(G * WAVE) void moe_gemm_k(
   const int nsteps = item_steps<NPW, SKW>(K);
   const int NT = PAIR ? 8 * NPW : 16 * NPW;         // output columns per item
   const int ntiles = (PAIR ? N / 2 : N) / NT;
-  const int nb0 = DENSE ? 1 : (s0.npad[0] >> 4);
-  const int nb1 = (DENSE || nsets < 2) ? 0 : (s1.npad[0] >> 4);
+  // both lists' num_post_pad in one round trip (a launch with one list passes it twice)
+  const int np0 = DENSE ? 16 : s0.npad[0];
+  const int np1 = DENSE ? 0 : s1.npad[0];
+  const int nb0 = np0 >> 4;
+  const int nb1 = (DENSE || nsets < 2) ? 0 : (np1 >> 4);
   const int nitems = (nb0 + nb1) * ntiles;
   const int ngroups = (nitems + IPG - 1) / IPG;
   float* sx = lds + (size_t)wv * nsteps * 16 * NH;

@@ -16,10 +16,10 @@
 //  * Routed / non-resident sets are 64-bit-word bitmaps built from wave ballots; misses are
 //    ranked in ascending expert id by popcount prefixes (no block scan).
 //  * Victims -- the nins smallest (stamp << 20 | slot) keys among slots whose expert is not
-//    routed, ascending -- are chosen by ONE wave with no barrier: a radix-style search for the
-//    nins-th smallest key (one ballot + popcount per slot register per key bit), a ballot
-//    compaction of the keys at or below it, and a rank of the <= nins survivors among
-//    themselves. Cost grows with key bits and nins, never with a per-insert block reduction,
+//    routed, ascending -- are chosen by ONE wave with no barrier: a radix search for the
+//    boundary stamp (8-bit digits counted in an LDS histogram, or one ballot + popcount per slot
+//    register per key bit for stamps past 32 bits), a ballot compaction of the keys at or below
+//    it, and a rank of the <= nins survivors among themselves. Cost grows with key bits and nins, never with a per-insert block reduction,
 //    so there is no insert-count cliff.
 //  * Align is stable at every mk: a token's rank inside its bucket is the number of earlier
 //    tokens routed to the same expert -- up to 256 tokens a popcount of the expert's token
@@ -120,7 +120,7 @@ __device__ __forceinline__ bool bit_of(const uint64_t* bm, int e) {
 //   * if the oldest group alone has >= nact slots (always at nact == 1, and the usual case
 //     in steady state, where a whole step's hits share one stamp), the victims are its first
 //     nact slots in slot order -- no search, no ranking;
-//   * otherwise a two-bit-per-round search over the stamp range finds the boundary stamp tau
+//   * otherwise a search over the stamp range, 8 bits per pass, finds the boundary stamp tau
 //     (#{stamp < tau} < nact <= #{stamp <= tau}); the boundary group is cut in slot order by
 //     ballot prefix, and the <= nact survivors are ranked among themselves.
 // Stamps outside [0, 2^43) fall back to a search over the reference key (stamp << 20) | slot
