@@ -17,8 +17,11 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
 // nearest-even float32 -> bfloat16 bits (NaN stays NaN)
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   const uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+  const uint32_t rne = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  const uint32_t qnan = (u >> 16) | 0x40u;
+  // a select, not a branch: the NaN test would otherwise split every conversion of a GEMM
+  // epilogue into two exec-masked paths
+  return (uint16_t)((u & 0x7fffffffu) > 0x7f800000u ? qnan : rne);
 }
 
 // two float32 -> two e4m3fn bytes (nearest-even), packed in the low 16 bits. Inputs are
