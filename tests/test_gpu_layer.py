@@ -351,6 +351,23 @@ def test_layer_prefill_read_through(pkg, pool):
         assert err <= TOL, f"step {t}: rel err {err:.3e}"
 
 
+def test_layer_prefill_threshold(pkg, pool):
+    """The layer switches to the prefill kernels at PREFILL_ROWS_PER_EXPERT routed rows per
+    expert (the measured crossover), counted on max_tokens x top_k: with 128 experts the
+    last decode size is 76 tokens (760 rows < 768) and 77 tokens (770 rows) is the first
+    prefill one; an explicit prefill_rows overrides it both ways."""
+    moe = pkg.moe
+    full = pkg.ExpertWeights(pool["w13"], pool["w13s"], pool["w2"], pool["w2s"])
+    hot = list(range(S))
+    slots = pkg.ExpertWeights(*[t[:S].to(DEV) for t in full.tensors()])   # slot i = expert i
+    assert moe.PREFILL_ROWS_PER_EXPERT * E == 768
+    mk = lambda M, **kw: pkg.LruMoELayer(full, hot, None, M, TOPK, DEV, slots=slots, **kw)
+    assert not mk(76).prefill
+    assert mk(77).prefill
+    assert mk(20, prefill_rows=200).prefill and not mk(20, prefill_rows=201).prefill
+    assert not mk(2048, prefill_rows=1 << 30).prefill
+
+
 def test_layer_prefill_graph_replay(pkg, pool):
     """A prefill-sized step (256 tokens, 2560 routed rows: the tiled kernels, gate_up with the
     activation in its epilogue) captured once as a HIP graph with the overlapped gather and
