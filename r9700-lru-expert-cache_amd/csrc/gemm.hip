@@ -38,6 +38,7 @@ namespace rlu {
 constexpr int GWV = 4;      // waves per workgroup
 constexpr int QIN_MAXG = 6;   // 128-column groups of the activation MODE 2 reads (K <= 768):
                               // its rows' loads stay live across the first weight steps
+static_assert(PMS >= QIN_MAXG, "item_mma_pm covers every K MODE 2 takes");
 constexpr int QIN_G = 4;      // waves per workgroup in MODE 2 (items of one block): with 8,
                               // 40 column tiles x 48 blocks leave CUs idle at B=4 (3.68 ms
                               // per 52-layer step against 3.57)
@@ -62,7 +63,7 @@ __global__ __launch_bounds__(G * WAVE) void moe_gemm_k(
   const int lane = lane_id();
   const int wv = uniform(threadIdx.x / WAVE);       // wave-uniform: item metadata in SGPRs
   const int sub = wv / SKW, ks = wv % SKW;
-  const int nsteps = item_steps<NPW, SKW>(K);
+  const int nsteps = AL ? PMS : item_steps<NPW, SKW>(K);   // AL: item_mma_pm's fixed steps
   const int NT = PAIR ? 8 * NPW : 16 * NPW;         // output columns per item
   const int ntiles = (PAIR ? N / 2 : N) / NT;
   // both lists' num_post_pad in one round trip (a launch with one list passes it twice)
@@ -175,10 +176,10 @@ __global__ __launch_bounds__(G * WAVE) void moe_gemm_k(
         }
         lds_barrier();
       };
+      static_assert(!AL || NPW == 4, "MODE 2 runs item_mma_pm: four strips as two pairs");
       if (live)
-        item_mma<NPW, SKW, DENSE, ring_of(NPW), PAIR, AL>(qx, xs, wq, ws, so, eid, n0, tw, mtk,
-                                                          top_k, K, N, ks, sx, acc, sod, twv,
-                                                          alds, als, xsl, pro, pre);
+        item_mma_pm(wq, ws, so, eid, n0, tw, mtk, K, N, sx, acc, sod, twv, alds, als, xsl, pro,
+                    pre);
       else {
         pre();
         pro();
@@ -248,7 +249,7 @@ int launch(int npw, int sk, int grid, hipStream_t st, const uint8_t* qx, const f
            int K, int N) {
   const int kpw = K / 128 / sk;
   const int d = ring_of(npw);
-  const int nsteps = (kpw + d - 1) / d * d;
+  const int nsteps = MODE == 2 ? PMS : (kpw + d - 1) / d * d;
   constexpr int G = MODE == 2 ? QIN_G : GWV;
   const size_t tail = MODE == 2 ? (size_t)16 * (K + 16) + (size_t)16 * (K / 128) * 4
                                 : (sk > 1 ? 2 * (size_t)G * npw * 4 * WAVE * 4 : 0);

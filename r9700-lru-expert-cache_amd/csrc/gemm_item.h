@@ -162,6 +162,85 @@ __device__ __forceinline__ void item_mma(const uint8_t* __restrict__ qx,
   for (int j = 0; j < D; ++j) step(j, c0 + j);
 }
 
+// The down projection's item from the A rows in LDS (item_mma with NPW 4, SKW 1, AL), with the
+// weight loads in the order they lie in memory. The wave's four strips (4 x 12 KB, adjacent)
+// go as two pairs, each pair's 24 KB front to back (step k of strips 2p and 2p + 1 side by
+// side), through a ring of PMS pair-steps: the first pair is issued whole, and the second
+// pair's loads go out as the first pair's steps are consumed. Read that way the wave's bytes
+// stream about 6% faster than step by step across all four strips (12 KB apart). Each strip
+// still accumulates its steps in ascending k from zero with the same scales, so the result
+// equals item_mma's bit for bit (K <= 128 PMS; steps past K / 128 carry zero scales and
+// repeat the last real step's operands, as item_mma's ring padding does).
+constexpr int PMS = 6;
+
+template <class PRO, class PRE>
+__device__ __forceinline__ void item_mma_pm(const uint8_t* __restrict__ wq,
+                                            const float* __restrict__ ws, int so, int eid,
+                                            int n0, const float* __restrict__ tw, int mtk, int K,
+                                            int N, float* sx, v4f (&acc)[4], int (&sod)[4],
+                                            float (&twv)[4], const uint8_t* alds, int als,
+                                            const float* xsl, const PRO& pro, const PRE& pre) {
+  const int lane = lane_id();
+  const int r16 = lane & 15, c4 = lane >> 4;
+  const int kpw = K / 128;
+  if (tw) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) twv[i] = tw[sod[i] < mtk ? sod[i] : 0];
+  }
+  const bool valid = so < mtk;
+  // weight-block scale of step k = 4 m + c4 (the four strips share one 128-column block)
+  const float* wsr = ws + ((size_t)eid * (N / 128) + n0 / 128) * kpw;
+  float xv[2], wv_[2];
+#pragma unroll
+  for (int m = 0; m < 2; ++m) wv_[m] = wsr[min(4 * m + c4, kpw - 1)];
+  const uint8_t* A = alds + (size_t)r16 * als + 16 * c4;
+  const uint8_t* W = wq + ((size_t)eid * N + n0) * K + lane * 16;
+  v4u rb[PMS][2][2];
+  auto issue = [&](int j, int t) __attribute__((always_inline)) {
+    const int p = t / PMS, k = min(t % PMS, kpw - 1);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const v4u* q = reinterpret_cast<const v4u*>(W + (size_t)(32 * p + 16 * s) * K +
+                                                  (size_t)k * 2048);
+      rb[j][s][0] = __builtin_nontemporal_load(q);
+      rb[j][s][1] = __builtin_nontemporal_load(q + 64);
+    }
+  };
+  auto step = [&](int j, int t) __attribute__((always_inline)) {
+    const int p = t / PMS, k = t % PMS;
+    const v4f f = *reinterpret_cast<const v4f*>(sx + k * 16 + 4 * c4);
+    const int ka = k < kpw ? k : kpw - 1;
+    const v8i av = pack8(*reinterpret_cast<const v4u*>(A + ka * 128),
+                         *reinterpret_cast<const v4u*>(A + ka * 128 + 64));
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const v4f d = mfma_f8(av, pack8(rb[j][s][0], rb[j][s][1]));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[2 * p + s][i] = fmaf(d[i], f[i], acc[2 * p + s][i]);
+    }
+  };
+  pre();
+#pragma unroll
+  for (int j = 0; j < PMS; ++j) issue(j, j);
+  pro();
+#pragma unroll
+  for (int m = 0; m < 2; ++m) xv[m] = xsl[(size_t)r16 * kpw + min(4 * m + c4, kpw - 1)];
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    const int k = 4 * m + c4;
+    if (k < PMS) sx[k * 16 + r16] = (k < kpw && valid) ? xv[m] * wv_[m] : 0.f;
+  }
+  wave_lds_sync();
+#pragma unroll
+  for (int t = 0; t < 2 * PMS; ++t) {
+    // the second pair reads A and the scales from LDS again: kept from the first pair they
+    // would hold 72 more registers and cost the second wave per SIMD
+    if (t == PMS) asm volatile("" ::: "memory");
+    step(t % PMS, t);
+    if (t + PMS < 2 * PMS) issue(t % PMS, t + PMS);
+  }
+}
+
 // Split-K: waves ks > 0 of each item add their partial sums into wave ks == 0 through LDS, in
 // split order (deterministic). rbuf: nwaves x NPW x 4 x 64 floats; every wave of the workgroup
 // takes part (one LDS barrier).
