@@ -257,8 +257,9 @@ def gemm_roofline(torch, pkg, layers, ids_last, rows, reps=3):
                 traffic_source=None if tr is None else tr["source"],
                 kernel=(f"rlu::moe_gemm_k (gate_up npw {layers[0].npw1} sk {layers[0].sk1}"
                         + (" with the SiLU-mul epilogue" if fused else "")
-                        + f", down npw {layers[0].npw2} sk {layers[0].sk2}"
-                        + (" quantizing the activation per workgroup" if fused else "")
+                        + (", down in 8-wave workgroups, 2 strips per wave, quantizing the "
+                           "activation per workgroup" if fused else
+                           f", down npw {layers[0].npw2} sk {layers[0].sk2}")
                         + "; hot + cold in one launch)"),
                 avg_launch_us=round(best, 2), algorithmic_bytes_per_launch=int(per_launch_bytes),
                 distinct_experts_per_layer=round(float(d.mean()), 1))

@@ -165,7 +165,7 @@ int rlu_moe_gemm_split_act(const void* qx, const float* xs, const void* wq_hot,
 /* No counterpart in the reference (see rlu_moe_gemm_split_act): the down projection of the split
  * GEMM reading the bf16 activation act [mtk, K] instead of q2 / s2. Each workgroup quantizes
  * the rows of its block per 128-column group exactly as rlu_silu_mul_quant (group 128) does,
- * so y equals rlu_moe_gemm_split (npw 4, sk 1, top_k 1) on that kernel's q2 / s2, bit for bit,
+ * so y equals rlu_moe_gemm_split (sk 1, any npw, top_k 1) on that kernel's q2 / s2, bit for bit,
  * with topk_weights as there. wq == NULL runs the hot list alone. K % 128 == 0, K <= 768,
  * N % 256 == 0; -1 / -2 on bad sizes or null operands. */
 int rlu_moe_gemm_split_qin(const void* act, const void* wq_hot, const float* ws_hot,

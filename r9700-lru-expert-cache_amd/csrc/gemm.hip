@@ -39,9 +39,17 @@ constexpr int GWV = 4;      // waves per workgroup
 constexpr int QIN_MAXG = 6;   // 128-column groups of the activation MODE 2 reads (K <= 768):
                               // its rows' loads stay live across the first weight steps
 static_assert(PMS >= QIN_MAXG, "item_mma_pm covers every K MODE 2 takes");
-constexpr int QIN_G = 4;      // waves per workgroup in MODE 2 (items of one block): with 8,
-                              // 40 column tiles x 48 blocks leave CUs idle at B=4 (3.68 ms
-                              // per 52-layer step against 3.57)
+// MODE 2's shape: workgroups of 8 waves, 2 strips (32 columns) per wave, so a workgroup covers
+// 256 columns of one block and quantizes the block's rows once for them; the wave's two strips
+// stream through a ring of 3 pair-steps (item_mma_pm). 127 registers: four waves per SIMD, so
+// both workgroups a CU can hold are resident and every live workgroup of a decode launch runs
+// at once. Measured on the 52-layer B=4 step against 4 waves x 4 strips with a 6-deep ring
+// (228 registers, two waves per SIMD): 3.305-3.308 against 3.348-3.352 ms; 4 waves x 2 strips:
+// 3.417-3.421; 8 waves x 2 strips with a 6-deep ring (three waves per SIMD, one workgroup per
+// CU): 3.432-3.441.
+constexpr int QIN_NPW = 2;    // strips per wave in MODE 2
+constexpr int QIN_RING = 3;   // pair-steps in MODE 2's weight ring
+constexpr int QIN_G = 8;      // waves per workgroup in MODE 2 (items of one block)
 
 // MODE 0: y [mtk, N] = the GEMM (routed weights optional).
 // MODE 1 (gate_up with its activation, NPW / 2 gate + NPW / 2 up strips per item): y
@@ -176,10 +184,10 @@ __global__ __launch_bounds__(G * WAVE) void moe_gemm_k(
         }
         lds_barrier();
       };
-      static_assert(!AL || NPW == 4, "MODE 2 runs item_mma_pm: four strips as two pairs");
+      static_assert(!AL || NPW % 2 == 0, "MODE 2 runs item_mma_pm: strips in pairs");
       if (live)
-        item_mma_pm(wq, ws, so, eid, n0, tw, mtk, K, N, sx, acc, sod, twv, alds, als, xsl, pro,
-                    pre);
+        item_mma_pm<NPW / 2, QIN_RING>(wq, ws, so, eid, n0, tw, mtk, K, N, sx, acc, sod, twv,
+                                       alds, als, xsl, pro, pre);
       else {
         pre();
         pro();
@@ -242,7 +250,7 @@ static int pick_sk(int nkg, int sk) {
   return 1;
 }
 
-// MODE 1 is built for npw 2 (any sk), MODE 2 for npw 4 with sk 1 (-6 / -4 otherwise).
+// MODE 1 is built for npw 2 (any sk), MODE 2 for npw QIN_NPW with sk 1 (-6 / -4 otherwise).
 template <bool DENSE, int MODE = 0>
 int launch(int npw, int sk, int grid, hipStream_t st, const uint8_t* qx, const float* xs,
            WSet s0, WSet s1, int nsets, uint16_t* y, const float* tw, int mtk, int top_k,
@@ -268,9 +276,9 @@ int launch(int npw, int sk, int grid, hipStream_t st, const uint8_t* qx, const f
     if (npw != 2) return -6;
     RLU_SK(2);
   } else if constexpr (MODE == 2) {
-    if (npw != 4) return -6;
+    if (npw != QIN_NPW) return -6;
     if (sk != 1) return -4;
-    RLU_L(4, 1);
+    RLU_L(QIN_NPW, 1);
   } else {
     switch (npw) {
       case 1: RLU_SK(1); break;
@@ -397,7 +405,7 @@ int rlu_moe_gemm_split_act(const void* qx, const float* xs, const void* wq_hot,
 // down of the split GEMM from the bf16 activation act [mtk, K] (rlu_moe_gemm_split_act's
 // output): each workgroup quantizes its block's rows per 128-column group as silu_mul_quant
 // does (same scales and codes) and runs the down GEMM on them, so y equals
-// rlu_moe_gemm_split (npw 4, sk 1) on silu_mul_quant's q2 / s2, bit for bit. Routed weights
+// rlu_moe_gemm_split (sk 1, any npw) on silu_mul_quant's q2 / s2, bit for bit. Routed weights
 // as there; wq == NULL runs the hot list alone. K <= 768, N % 256 == 0.
 int rlu_moe_gemm_split_qin(const void* act, const void* wq_hot, const float* ws_hot,
                            const int* sorted_hot, const int* eids_hot, const int* npad_hot,
@@ -409,15 +417,15 @@ int rlu_moe_gemm_split_qin(const void* act, const void* wq_hot, const float* ws_
   if (!act || !wq_hot || !ws_hot || !sorted_hot || !eids_hot || !npad_hot || !y) return -1;
   const int nsets = wq ? 2 : 1;
   if (nsets == 2 && (!ws || !sorted_cold || !eids_cold || !npad_cold)) return -1;
-  if (K % 128 || N % (64 * rlu::QIN_G) || K > 128 * rlu::QIN_MAXG) return -2;
+  if (K % 128 || N % (16 * rlu::QIN_NPW * rlu::QIN_G) || K > 128 * rlu::QIN_MAXG) return -2;
   if (mtk == 0) return 0;
   const int nb = (em + 15) / 16;
   const int nblive = nsets * nb < mtk ? nsets * nb : mtk;
-  const int items = nblive * (N / 64);
+  const int items = nblive * (N / (16 * rlu::QIN_NPW));
   const int grid = ((items + rlu::QIN_G - 1) / rlu::QIN_G + 7) / 8 * 8;   // XCD-aware order
   const rlu::WSet s0{(const uint8_t*)wq_hot, ws_hot, sorted_hot, eids_hot, npad_hot};
   const rlu::WSet s1{(const uint8_t*)wq, ws, sorted_cold, eids_cold, npad_cold};
-  return rlu::launch<false, 2>(4, 1, grid, stream, (const uint8_t*)act, nullptr, s0,
+  return rlu::launch<false, 2>(rlu::QIN_NPW, 1, grid, stream, (const uint8_t*)act, nullptr, s0,
                                nsets == 2 ? s1 : s0, nsets, (uint16_t*)y, topk_weights, mtk, 1,
                                K, N);
 }

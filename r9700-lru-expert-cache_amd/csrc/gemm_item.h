@@ -162,22 +162,21 @@ __device__ __forceinline__ void item_mma(const uint8_t* __restrict__ qx,
   for (int j = 0; j < D; ++j) step(j, c0 + j);
 }
 
-// The down projection's item from the A rows in LDS (item_mma with NPW 4, SKW 1, AL), with the
-// weight loads in the order they lie in memory. The wave's four strips (4 x 12 KB, adjacent)
-// go as two pairs, each pair's 24 KB front to back (step k of strips 2p and 2p + 1 side by
-// side), through a ring of PMS pair-steps: the first pair is issued whole, and the second
-// pair's loads go out as the first pair's steps are consumed. Read that way the wave's bytes
-// stream about 6% faster than step by step across all four strips (12 KB apart). Each strip
-// still accumulates its steps in ascending k from zero with the same scales, so the result
-// equals item_mma's bit for bit (K <= 128 PMS; steps past K / 128 carry zero scales and
-// repeat the last real step's operands, as item_mma's ring padding does).
+// The down projection's item from the A rows in LDS (item_mma with SKW 1 and AL), with the
+// weight loads in the order they lie in memory. The wave's 2 NP strips (12 KB each, adjacent)
+// go as NP pairs, each pair's 24 KB front to back (step k of strips 2p and 2p + 1 side by
+// side), through a ring of R pair-steps that runs on across the pairs. Read that way a wave of
+// four strips streams its bytes about 6% faster than step by step across all four (12 KB
+// apart). Each strip still accumulates its steps in ascending k from zero with the same
+// scales, so the result equals item_mma's bit for bit (K <= 128 PMS; steps past K / 128 carry
+// zero scales and repeat the last real step's operands, as item_mma's ring padding does).
 constexpr int PMS = 6;
 
-template <class PRO, class PRE>
+template <int NP, int R, class PRO, class PRE>
 __device__ __forceinline__ void item_mma_pm(const uint8_t* __restrict__ wq,
                                             const float* __restrict__ ws, int so, int eid,
                                             int n0, const float* __restrict__ tw, int mtk, int K,
-                                            int N, float* sx, v4f (&acc)[4], int (&sod)[4],
+                                            int N, float* sx, v4f (&acc)[2 * NP], int (&sod)[4],
                                             float (&twv)[4], const uint8_t* alds, int als,
                                             const float* xsl, const PRO& pro, const PRE& pre) {
   const int lane = lane_id();
@@ -195,7 +194,7 @@ __device__ __forceinline__ void item_mma_pm(const uint8_t* __restrict__ wq,
   for (int m = 0; m < 2; ++m) wv_[m] = wsr[min(4 * m + c4, kpw - 1)];
   const uint8_t* A = alds + (size_t)r16 * als + 16 * c4;
   const uint8_t* W = wq + ((size_t)eid * N + n0) * K + lane * 16;
-  v4u rb[PMS][2][2];
+  v4u rb[R][2][2];
   auto issue = [&](int j, int t) __attribute__((always_inline)) {
     const int p = t / PMS, k = min(t % PMS, kpw - 1);
 #pragma unroll
@@ -221,7 +220,7 @@ __device__ __forceinline__ void item_mma_pm(const uint8_t* __restrict__ wq,
   };
   pre();
 #pragma unroll
-  for (int j = 0; j < PMS; ++j) issue(j, j);
+  for (int j = 0; j < R; ++j) issue(j, j);
   pro();
 #pragma unroll
   for (int m = 0; m < 2; ++m) xv[m] = xsl[(size_t)r16 * kpw + min(4 * m + c4, kpw - 1)];
@@ -232,12 +231,12 @@ __device__ __forceinline__ void item_mma_pm(const uint8_t* __restrict__ wq,
   }
   wave_lds_sync();
 #pragma unroll
-  for (int t = 0; t < 2 * PMS; ++t) {
-    // the second pair reads A and the scales from LDS again: kept from the first pair they
+  for (int t = 0; t < NP * PMS; ++t) {
+    // a later pair reads A and the scales from LDS again: kept from the first pair they
     // would hold 72 more registers and cost the second wave per SIMD
-    if (t == PMS) asm volatile("" ::: "memory");
-    step(t % PMS, t);
-    if (t + PMS < 2 * PMS) issue(t % PMS, t + PMS);
+    if (t > 0 && t % PMS == 0) asm volatile("" ::: "memory");
+    step(t % R, t);
+    if (t + R < NP * PMS) issue(t % R, t + R);
   }
 }
 

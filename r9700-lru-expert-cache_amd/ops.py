@@ -192,9 +192,9 @@ def moe_gemm_split_qin(y: torch.Tensor, act: torch.Tensor, w_hot: torch.Tensor,
                        s_hot: torch.Tensor, align_hot, topk_weights: torch.Tensor | None,
                        mtk: int, w_cold: torch.Tensor | None = None,
                        s_cold: torch.Tensor | None = None, align_cold=None) -> None:
-    """down of the split GEMM (npw 4, sk 1) from the bf16 activation [mtk, K]: each
-    workgroup quantizes its block's rows as silu_mul_quant (group 128) does, so y [mtk, N]
-    equals the split GEMM on that kernel's q2 / s2, bit for bit."""
+    """down of the split GEMM (sk 1) from the bf16 activation [mtk, K]: each workgroup (8
+    waves, 256 columns of one block) quantizes its block's rows as silu_mul_quant (group 128)
+    does, so y [mtk, N] equals the split GEMM on that kernel's q2 / s2, bit for bit."""
     N, K = w_hot.shape[1], w_hot.shape[2]
     assert y.shape == (mtk, N) and y.dtype == torch.bfloat16 and y.is_contiguous()
     assert act.shape == (mtk, K) and act.dtype == torch.bfloat16 and act.is_contiguous()
