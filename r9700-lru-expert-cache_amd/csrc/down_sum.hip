@@ -11,11 +11,12 @@
 // the same per-step fma as moe_gemm_k, multiplies by the routed weight and rounds to bf16; the
 // strip's values are then added in k order into one float32 sum. The token's activation
 // fragments for every K step are loaded once and serve all its experts; the weights stream
-// through a ring of NS stages (one expert's K range) that runs on across a wave's experts, so
-// expert k + 1's strip is in flight while expert k is summed. With the experts split over two
-// waves per strip (KSPLIT) a workgroup keeps twice the weight bytes in flight: the kernel is
-// bound by its loads' latency at these few tokens. Experts come from the layer's cache table: a resident expert from its
-// slot, any other from the full tensor (device or pinned host memory).
+// through a ring of RE x NS stages (RE experts' K ranges) that runs on across a wave's
+// experts, so the next RE experts' strips are in flight while expert k is summed. With the
+// experts split over two waves per strip (KSPLIT) a workgroup keeps twice the weight bytes in
+// flight: the kernel is bound by its loads' latency at these few tokens. Experts come from the
+// layer's cache table: a resident expert from its slot, any other from the full tensor
+// (device or pinned host memory).
 //
 // Each expert strip is read once per token that routes to it; workgroups are laid out so that
 // the tokens of one column range run on one XCD at the same time and share its L2. The ACT form
@@ -36,6 +37,8 @@ constexpr int BUF_WORD3 = 0x00020000;      // raw buffer descriptor word 3 on gf
 constexpr int NTP = 2;                     // buffer cache policy: streaming
 constexpr int MAXK = 16;                   // top_k the kernel takes (A rows of one MFMA)
 constexpr int KSPLIT = 2;                  // waves per column strip (the experts split)
+constexpr int RE = 2;                      // experts of a wave in flight at once: B=1 step
+                                           // 2.588-2.591 -> 2.579-2.582 ms (3 deep: 2.588)
 
 // ACT: qa is the bf16 activation [M top_k, K] (the SiLU-mul output) and sa is not read; the
 // workgroup quantizes the token's rows per 128-column group into LDS first, exactly as
@@ -98,11 +101,11 @@ __global__ __launch_bounds__(W * KS * WAVE) void down_sum_k(
       ra[j][1] = *reinterpret_cast<const v4u*>(p + 64);
     }
   }
-  v4u rb[NS][2];
+  v4u rb[RE][NS][2];
   const int voff = lane * 16;
-  auto issue = [&](int j, __amdgpu_buffer_rsrc_t b) __attribute__((always_inline)) {
-    rb[j][0] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(b, voff, j * 2048, NTP));
-    rb[j][1] = __builtin_bit_cast(
+  auto issue = [&](int x, int j, __amdgpu_buffer_rsrc_t b) __attribute__((always_inline)) {
+    rb[x][j][0] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(b, voff, j * 2048, NTP));
+    rb[x][j][1] = __builtin_bit_cast(
         v4u, __builtin_amdgcn_raw_buffer_load_b128(b, voff + 1024, j * 2048, NTP));
   };
   auto wbuf = [&](int kk) __attribute__((always_inline)) {
@@ -141,7 +144,9 @@ __global__ __launch_bounds__(W * KS * WAVE) void down_sum_k(
     }
   }
 #pragma unroll
-  for (int j = 0; j < NS; ++j) issue(j, wbuf(0));
+  for (int x = 0; x < RE; ++x)
+#pragma unroll
+    for (int j = 0; j < NS; ++j) issue(x, j, wbuf(x));
   if constexpr (ACT) {
 #pragma unroll
     for (int p = 0; p < NPASS; ++p) {
@@ -171,16 +176,17 @@ __global__ __launch_bounds__(W * KS * WAVE) void down_sum_k(
   for (int kk = 0; kk < TKH; ++kk) {
     const int q = kk & 1;
     load_scales(kk + 1, q ^ 1);
-    const __amdgpu_buffer_rsrc_t bn = wbuf(kk + 1);
+    const __amdgpu_buffer_rsrc_t bn = wbuf(kk + RE);   // past the last: no records, no reads
+    const int xr = kk % RE;
     v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
       const float f = fx[q][j] * fw[q][j];
-      const v4f d = mfma_f8(pack8(ra[j][0], ra[j][1]), pack8(rb[j][0], rb[j][1]));
+      const v4f d = mfma_f8(pack8(ra[j][0], ra[j][1]), pack8(rb[xr][j][0], rb[xr][j][1]));
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc[i] = fmaf(d[i], f, acc[i]);
       asm volatile("" : "+v"(acc));
-      issue(j, bn);
+      issue(xr, j, bn);
       __builtin_amdgcn_sched_barrier(0);
     }
     // row k sits in lanes c4 = k / 4, element k % 4: round it as the GEMM epilogue does, then

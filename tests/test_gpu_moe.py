@@ -468,7 +468,7 @@ def test_moe_gemm_split_one_launch_equals_two_calls(pkg, ops, layer):
 # ---- gate_up with its activation, down from the activation (decode) -------------------------
 @pytest.mark.parametrize("M,sk,pinned,holes", [(1, 1, False, False), (5, 1, True, False),
                                                (20, 2, False, False), (20, 2, True, True),
-                                               (20, 4, False, False)])
+                                               (20, 4, False, False), (64, 2, False, False)])
 def test_moe_gemm_split_act_and_qin_equal_the_unfused_path(pkg, ops, layer, M, sk, pinned,
                                                             holes):
     """gate_up with SiLU-mul in its epilogue (rlu_moe_gemm_split_act) equals the split gate_up
@@ -476,7 +476,8 @@ def test_moe_gemm_split_act_and_qin_equal_the_unfused_path(pkg, ops, layer, M, s
     activation per workgroup (rlu_moe_gemm_split_qin) equals the split down GEMM on
     silu_mul_quant's q2 / s2, bit for bit: hot slots + cold full tensor (device or pinned host
     memory), and with holes (every other hot block's expert id set to -1, as the gather
-    overlap's resident bucket has them) then the hot list alone over the other blocks."""
+    overlap's resident bucket has them) then the hot list alone over the other blocks. At 64
+    tokens (640 rows over 40 experts) down has more 8-wave workgroups than a GPU holds at once."""
     E, H, I = layer["E"], layer["H"], layer["I"]
     top_k = 10
     ids = routing(M, top_k, E, seed=M + 61)
