@@ -303,6 +303,14 @@ int rlu_route_capture(const int* topk_ids, int n, int layer, int nlayer, int rin
                       short* ring_ids, long long* ring_step, long long* ctr,
                       hipStream_t stream);
 
+/* No counterpart in the reference: a self-test for callers who check the device before use.
+ * The prefill SiLU-mul-quant epilogue rounds float32 to bfloat16 with gfx950's one-instruction
+ * conversion, where every other kernel uses an integer nearest-even rounding; this runs both
+ * over all 2^32 float32 bit patterns and adds the number that differ to *bad (the caller
+ * zeroes it). 0 means the kernels' results do not depend on which rounding they use. Returns
+ * -1 for a null pointer, else the launch status. */
+int rlu_selftest_bf16(unsigned long long* bad, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

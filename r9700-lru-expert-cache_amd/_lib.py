@@ -44,6 +44,7 @@ SIGNATURES: dict[str, tuple] = {
     "rlu_moe_down_sum": (_I, [_P] * 10 + [_I] * 5 + [_P]),
     "rlu_moe_down_sum_act": (_I, [_P] * 9 + [_I] * 5 + [_P]),
     "rlu_route_capture": (_I, [_P] + [_I] * 5 + [_P] * 4),
+    "rlu_selftest_bf16": (_I, [_P, _P]),
 }
 
 

@@ -24,6 +24,19 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   return (uint16_t)((u & 0x7fffffffu) > 0x7f800000u ? qnan : rne);
 }
 
+// f32_to_bf16 in one instruction: gfx950's v_cvt_pk_bf16_f32 gives the same bits for every
+// one of the 2^32 float32 inputs (nearest even; NaN payload kept with the quiet bit set;
+// denormals rounded, not flushed), which the library's self-test rlu_selftest_bf16 checks
+// on the device. Inline assembly: clang's vector conversion to __bf16 did not lower to it
+// correctly (it dropped one element of a pair). Used where the rounding sits on a kernel's
+// critical path (the prefill SiLU-mul-quant epilogue); elsewhere a faster epilogue only bunched
+// the stores that follow it and measured slower.
+__device__ __forceinline__ uint16_t f32_to_bf16_hw(float f) {
+  uint32_t r;
+  asm("v_cvt_pk_bf16_f32 %0, %1, 0" : "=v"(r) : "v"(f));
+  return (uint16_t)r;
+}
+
 // two float32 -> two e4m3fn bytes (nearest-even), packed in the low 16 bits. Inputs are
 // already clamped to +-448 by every caller, so saturation behaviour never comes into play.
 __device__ __forceinline__ uint32_t f32x2_to_e4m3(float a, float b) {
@@ -58,6 +71,12 @@ __device__ __forceinline__ float exp_f32(float x) {
 __device__ __forceinline__ float silu_bf16(float g) {
   const float s = __fdiv_rn(g, __fadd_rn(1.0f, exp_f32(-g)));
   return bf16_to_f32(f32_to_bf16(s));
+}
+
+// silu_bf16 with the one-instruction rounding (the same bits)
+__device__ __forceinline__ float silu_bf16_hw(float g) {
+  const float s = __fdiv_rn(g, __fadd_rn(1.0f, exp_f32(-g)));
+  return bf16_to_f32(f32_to_bf16_hw(s));
 }
 
 }  // namespace rlu

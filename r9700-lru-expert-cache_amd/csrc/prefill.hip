@@ -409,7 +409,7 @@ __global__ __launch_bounds__(W * WAVE) void stream_k(
                   const int rr = t * 16 + 4 * c4 + i;
 #pragma unroll
                   for (int s = 0; s < S; ++s)
-                    ot[rr * C + (w * S + s) * 16 + r16] = f32_to_bf16(acc[bk][s][i]);
+                    ot[rr * C + (w * S + s) * 16 + r16] = f32_to_bf16_hw(acc[bk][s][i]);
                 }
               }
             }
@@ -426,7 +426,7 @@ __global__ __launch_bounds__(W * WAVE) void stream_k(
               uint32_t mx = 0;
 #pragma unroll
               for (int j = 0; j < 8; ++j) {
-                a[j] = bf16_to_f32(f32_to_bf16(__fmul_rn(silu_bf16(gv[j]), uv[j])));
+                a[j] = bf16_to_f32(f32_to_bf16_hw(__fmul_rn(silu_bf16_hw(gv[j]), uv[j])));
                 mx = max(mx, abs_bits(a[j]));
               }
               const float sc = scale_of(row_max_u32(mx));

@@ -216,6 +216,18 @@ __global__ __launch_bounds__(SUM_THR) void moe_sum_k(const uint16_t* __restrict_
   *reinterpret_cast<uint4*>(out + (size_t)m * H + c) = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
+// Self-test of f32_to_bf16_hw: every float32 bit pattern through both roundings; a thread
+// takes patterns 2 t and 2 t + 1 (opaque to the compiler, so nothing is folded between them)
+// and counts the patterns whose two results differ.
+__global__ __launch_bounds__(256) void bf16_selftest_k(unsigned long long* __restrict__ bad) {
+  const uint32_t t = blockIdx.x * 256u + threadIdx.x;     // 0 .. 2^31 - 1
+  uint32_t u0 = 2u * t, u1 = 2u * t + 1u;
+  asm volatile("" : "+v"(u0), "+v"(u1));
+  const float a = __uint_as_float(u0), b = __uint_as_float(u1);
+  const int n = (f32_to_bf16_hw(a) != f32_to_bf16(a)) + (f32_to_bf16_hw(b) != f32_to_bf16(b));
+  if (n) atomicAdd(bad, (unsigned long long)n);
+}
+
 }  // namespace rlu
 
 extern "C" {
@@ -258,6 +270,15 @@ int rlu_moe_sum(const void* in, int M, int top_k, int H, void* out, hipStream_t 
   hipLaunchKernelGGL(rlu::moe_sum_k, dim3(M, (H + rlu::SUM_THR * 8 - 1) / (rlu::SUM_THR * 8)),
                      dim3(rlu::SUM_THR), 0, stream, (const uint16_t*)in, top_k, H,
                      (uint16_t*)out);
+  return (int)hipGetLastError();
+}
+
+// Counts the float32 inputs (of all 2^32) on which f32_to_bf16_hw and f32_to_bf16 differ into
+// *bad (which the caller zeroes); 0 means the one-instruction rounding may stand in for the
+// integer one. Returns -1 for a null pointer, else the launch status.
+int rlu_selftest_bf16(unsigned long long* bad, hipStream_t stream) {
+  if (!bad) return -1;
+  hipLaunchKernelGGL(rlu::bf16_selftest_k, dim3(1u << 23), dim3(256), 0, stream, bad);
   return (int)hipGetLastError();
 }
 

@@ -103,3 +103,19 @@ def test_quant_equals_ieee_division_on_every_input(pkg, domain):
     assert pairs >= (2 * 532668480 if domain == "finite" else 2 * 130000)
     assert bad_s == 0, f"{bad_s} scales differ from amax / 448"
     assert bad_q == 0, f"{bad_q} codes differ from the IEEE-division quant"
+
+
+def test_bf16_rounding_one_instruction_equals_integer_rounding(pkg):
+    """The prefill SiLU-mul-quant epilogue rounds float32 to bf16 with gfx950's
+    v_cvt_pk_bf16_f32; every other kernel, and the oracle, with integer nearest-even rounding
+    (NaN kept, quiet bit set). rlu_selftest_bf16 runs both over all 2^32 float32 bit patterns:
+    not one may differ, or the prefill layer's bits would depend on which kernel ran."""
+    import ctypes
+    bad = torch.zeros(1, dtype=torch.int64, device=DEV)
+    gpu_case("bf16 rounding self-test over 2^32 inputs")
+    rc = pkg.lib().rlu_selftest_bf16(ctypes.c_void_p(bad.data_ptr()),
+                                     ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert int(bad.item()) == 0
+    assert pkg.lib().rlu_selftest_bf16(None, None) == -1
