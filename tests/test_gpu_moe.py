@@ -87,10 +87,11 @@ def test_group_quant_bitexact(ops, rows, K, group):
 
 
 # H 7168: 14 one-wave workgroups per row; H 8 and 64: one partly idle wave; top_k 12: the
-# ten-row batch and then the tail rows one at a time
+# ten-row batch and then the tail rows one at a time; 4096 x 10 x 2560: a prefill chunk's
+# moe_sum
 @pytest.mark.parametrize("M,top_k,H", [(5, 10, 2560), (20, 10, 2560), (1, 1, 64), (3, 7, 1024),
                                        (7, 10, 7168), (2, 3, 8), (9, 12, 2560),
-                                       (1024, 10, 2560)])
+                                       (1024, 10, 2560), (4096, 10, 2560)])
 def test_moe_sum_bitexact(ops, M, top_k, H):
     rng = np.random.default_rng(M * top_k)
     ic3 = fp8.bf16_round(rng.standard_normal((M * top_k, H)).astype(np.float32))
