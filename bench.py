@@ -498,6 +498,13 @@ def prefill_gemm(torch, pkg, dev, T=4096, reps=3, lru=True, wv=0):
         res["layer_step"] = ("LruMoELayer.apply on the chunk: fused LRU + align + quant, gate_up "
                              "with SiLU-mul-quant, down, moe_sum")
         del layer
+        # the same chunk through a layer of 257 slots (the decode workload's cache size): 257
+        # experts' rows come from the slots, the other 255 experts' from the full tensor, and
+        # each GEMM covers both aligns in one launch
+        layer = pkg.LruMoELayer(full, range(257), None, T, TOPK, dev)
+        res["layer_step_257_slots_us"] = round(timed(lambda: layer.apply(out, hs, twl, ids_t,
+                                                                           gather=False)), 1)
+        del layer
     del w13, w2
     torch.cuda.empty_cache()
     return res

@@ -226,6 +226,39 @@ int rlu_moe_gemm_fp8blk_tiled_silu_quant(const void* qx, const float* xs, const 
                                          const int* ntiles, int max_tiles, void* q2, float* s2,
                                          int mtk, int top_k, int K, int N, hipStream_t stream);
 
+/* No counterpart in the reference (its _gemm_split, r4d_mxfp4_moe.py.lru.diff:584-593, makes
+ * one r4d_mxfp4_moe_gemm_into call per align): the prefill GEMMs over both of a layer's
+ * aligns in one launch -- align 0 over weights wq0 / ws0 (the resident slots), align
+ * 1 over wq1 / ws1 (the full tensor the non-resident experts are read from, device or pinned
+ * host memory), both indexing the rows of qx and writing the same output.
+ *   rlu_moe_gemm_tiles_split: the tile list of both aligns, align 0's tiles then align 1's with
+ *     bit 16 of the block count set; tiles holds 2 (nb_max0 + nb_max1) ints; nb_max <= 8192
+ *     each (-1 otherwise, or on a NULL pointer).
+ *   rlu_moe_gemm_fp8blk_tiled_split / _split_silu_quant: rlu_moe_gemm_fp8blk_tiled (wv = 0) /
+ *     rlu_moe_gemm_fp8blk_tiled_silu_quant on each align, in one launch, equal to the two calls
+ *     bit for bit; max_tiles = nb_max0 + nb_max1. Built for the streamed kernel's shapes (K =
+ *     2560 or 768 and N % 256 == 0; K = 2560 for _silu_quant): other shapes return -6 before
+ *     any other check, so a call with mtk = 0 is a capability query. Every pointer but
+ *     topk_weights is required (-1); otherwise -1 / -2 as rlu_moe_gemm_fp8blk_tiled. */
+int rlu_moe_gemm_tiles_split(const int* expert_ids0, const int* num_post_pad0, int nb_max0,
+                             const int* expert_ids1, const int* num_post_pad1, int nb_max1,
+                             int* tiles, int* ntiles, hipStream_t stream);
+int rlu_moe_gemm_fp8blk_tiled_split(const void* qx, const float* xs, const void* wq0,
+                                    const float* ws0, const int* sorted_ids0,
+                                    const int* expert_ids0, const void* wq1, const float* ws1,
+                                    const int* sorted_ids1, const int* expert_ids1,
+                                    const int* tiles, const int* ntiles, int max_tiles,
+                                    const float* topk_weights, void* y, int mtk, int top_k,
+                                    int K, int N, hipStream_t stream);
+int rlu_moe_gemm_fp8blk_tiled_split_silu_quant(const void* qx, const float* xs, const void* wq0,
+                                               const float* ws0, const int* sorted_ids0,
+                                               const int* expert_ids0, const void* wq1,
+                                               const float* ws1, const int* sorted_ids1,
+                                               const int* expert_ids1, const int* tiles,
+                                               const int* ntiles, int max_tiles, void* q2,
+                                               float* s2, int mtk, int top_k, int K, int N,
+                                               hipStream_t stream);
+
 /* No counterpart in the reference (which runs the down GEMM into ic3 and then vLLM's moe_sum,
  * r4d_mxfp4_moe.py.lru.diff:690-696): the decode down projection with moe_sum folded in.
  * out[t] (bf16 [M, N]) = sum over k in k order, in float32, of bf16(down row (t, k) x

@@ -41,6 +41,10 @@ SIGNATURES: dict[str, tuple] = {
     "rlu_moe_gemm_fp8blk_tiled": (_I, [_P] * 8 + [_I, _P, _P] + [_I] * 5 + [_P]),
     "rlu_moe_gemm_fp8blk_tiled_noalloc": (_I, [_P] * 7 + [_I, _P, _P] + [_I] * 5 + [_P]),
     "rlu_moe_gemm_fp8blk_tiled_silu_quant": (_I, [_P] * 8 + [_I, _P, _P] + [_I] * 4 + [_P]),
+    "rlu_moe_gemm_tiles_split": (_I, [_P, _P, _I, _P, _P, _I, _P, _P, _P]),
+    "rlu_moe_gemm_fp8blk_tiled_split": (_I, [_P] * 12 + [_I, _P, _P] + [_I] * 4 + [_P]),
+    "rlu_moe_gemm_fp8blk_tiled_split_silu_quant": (_I, [_P] * 12 + [_I, _P, _P] + [_I] * 4 +
+                                                   [_P]),
     "rlu_moe_down_sum": (_I, [_P] * 10 + [_I] * 5 + [_P]),
     "rlu_moe_down_sum_act": (_I, [_P] * 9 + [_I] * 5 + [_P]),
     "rlu_route_capture": (_I, [_P] + [_I] * 5 + [_P] * 4),

@@ -4,7 +4,9 @@
 //   tiles_k        from moe_align_block_size output (expert_ids per 16-row block, num_post_pad)
 //                  builds the tile list: each run of blocks of one expert is cut into tiles of
 //                  at most TMB blocks; a tile is (first block, block count). Blocks of expert -1
-//                  make no tile.
+//                  make no tile. Given two aligns (a layer's resident and non-resident rows),
+//                  it lists the second one's tiles after the first one's, with bit 16 of the
+//                  block count set; only the streamed kernel (prefill.hip) reads such a list.
 //   tiled_k        one workgroup (8 waves) computes a TMB*16-row x 256-column tile: per 128-deep
 //                  K step it stages the tile's activation rows (gathered through sorted_ids) and
 //                  the 16 weight strips (fragment order, 2 KB contiguous each) in LDS, double-
@@ -37,16 +39,13 @@ constexpr int TB_THR = 1024;
 constexpr int NXCD = 8;          // XCDs of an MI355X
 
 // ---- tile list ---------------------------------------------------------------------------
-__global__ __launch_bounds__(TB_THR) void tiles_k(const int* __restrict__ eids,
-                                                  const int* __restrict__ npad, int nb_max,
-                                                  int* __restrict__ tiles,
-                                                  int* __restrict__ ntiles) {
-  constexpr int NW = TB_THR / WAVE;
-  __shared__ int se[MAXNB];
-  __shared__ int wtot[2][NW];                       // per wave: max of run starts, tile count
+// The tiles of one align, written from tile index base on with the list number in bit 16 of
+// the block count; returns base plus their count (to every thread). se / wtot are the
+// workgroup's LDS; the call ends with a barrier, so the next list may rewrite them.
+__device__ __forceinline__ int list_tiles(const int* __restrict__ eids, int nb, int list, int base,
+                                          int* se, int (*wtot)[TB_THR / WAVE], int* done,
+                                          int* __restrict__ tiles) {
   const int t = threadIdx.x, lane = lane_id(), wv = t / WAVE;
-  int nb = npad[0] >> 4;
-  nb = nb < nb_max ? nb : nb_max;
   for (int b = t; b < nb; b += TB_THR) se[b] = eids[b];
   __syncthreads();
   const int per = (nb + TB_THR - 1) / TB_THR;
@@ -77,7 +76,7 @@ __global__ __launch_bounds__(TB_THR) void tiles_k(const int* __restrict__ eids,
   __syncthreads();
   int psum = 0;
   for (int i = 0; i < wv; ++i) psum += wtot[1][i];
-  int pos = psum + wsum - cnt;
+  int pos = base + psum + wsum - cnt;
   rs = carry;
   for (int b = lo; b < hi; ++b) {
     if (b == 0 || se[b] != se[b - 1]) rs = b;
@@ -85,11 +84,33 @@ __global__ __launch_bounds__(TB_THR) void tiles_k(const int* __restrict__ eids,
       int n = 1;
       while (n < TMB && b + n < nb && se[b + n] == se[b]) ++n;
       tiles[2 * pos] = b;
-      tiles[2 * pos + 1] = n;
+      tiles[2 * pos + 1] = n | list << 16;
       ++pos;
     }
   }
-  if (t == TB_THR - 1) ntiles[0] = psum + wsum;
+  if (t == TB_THR - 1) *done = base + psum + wsum;
+  __syncthreads();
+  return *done;
+}
+
+// The tile list of align 0 (eids0) and, when eids1 is given, of align 1 after it: a tile is
+// (first block, block count | align << 16), at most 8 blocks of one expert.
+__global__ __launch_bounds__(TB_THR) void tiles_k(const int* __restrict__ eids0,
+                                                  const int* __restrict__ npad0, int nb_max0,
+                                                  const int* __restrict__ eids1,
+                                                  const int* __restrict__ npad1, int nb_max1,
+                                                  int* __restrict__ tiles,
+                                                  int* __restrict__ ntiles) {
+  __shared__ int se[MAXNB];
+  __shared__ int wtot[2][TB_THR / WAVE];            // per wave: max of run starts, tile count
+  __shared__ int done;
+  const int nb0 = min(npad0[0] >> 4, nb_max0);
+  int n = list_tiles(eids0, nb0, 0, 0, se, wtot, &done, tiles);
+  if (eids1) {
+    const int nb1 = min(npad1[0] >> 4, nb_max1);
+    n = list_tiles(eids1, nb1, 1, n, se, wtot, &done, tiles);
+  }
+  if (threadIdx.x == 0) ntiles[0] = n;
 }
 
 // ---- the tiled GEMM ------------------------------------------------------------------------
@@ -280,9 +301,9 @@ static void launch_tiled(const void* qx, const float* xs, const void* wq, const 
                          const int* sorted_ids, const int* expert_ids, const int* tiles,
                          const int* ntiles, int max_tiles, const float* topk_weights, void* y,
                          int mtk, int top_k, int K, int N, int wv, hipStream_t stream) {
-  if (wv == 0 && rlu::launch_prefill_stream(qx, xs, wq, ws, sorted_ids, expert_ids, tiles,
-                                            ntiles, max_tiles, topk_weights, y, mtk, top_k, K,
-                                            N, stream) == 0)
+  if (wv == 0 && rlu::launch_prefill_stream(qx, xs, wq, ws, sorted_ids, expert_ids, nullptr,
+                                            tiles, ntiles, max_tiles, topk_weights, y, mtk,
+                                            top_k, K, N, stream) == 0)
     return;
   const int items = max_tiles * (N / TBN);
   int grid = rlu::device_cus() * (wv ? wv : 2);
@@ -310,7 +331,7 @@ int rlu_moe_gemm_tiles(const int* expert_ids, const int* num_post_pad, int nb_ma
   if (nb_max <= 0 || nb_max > MAXNB || !expert_ids || !num_post_pad || !tiles || !ntiles)
     return -1;
   hipLaunchKernelGGL(tiles_k, dim3(1), dim3(TB_THR), 0, stream, expert_ids, num_post_pad, nb_max,
-                     tiles, ntiles);
+                     nullptr, nullptr, 0, tiles, ntiles);
   return (int)hipGetLastError();
 }
 
@@ -346,7 +367,7 @@ int rlu_moe_gemm_fp8blk_tiled_noalloc(const void* qx, const float* xs, const voi
   if (e) return e;
   int* ws_count = ws_tiles + 2 * MAXNB;
   hipLaunchKernelGGL(tiles_k, dim3(1), dim3(TB_THR), 0, stream, expert_ids, num_post_pad, nb,
-                     ws_tiles, ws_count);
+                     nullptr, nullptr, 0, ws_tiles, ws_count);
   launch_tiled(qx, xs, wq, ws, sorted_ids, expert_ids, ws_tiles, ws_count, nb, topk_weights, y,
                mtk, top_k, K, N, wv, stream);
   return (int)hipGetLastError();
@@ -369,8 +390,75 @@ int rlu_moe_gemm_fp8blk_tiled_silu_quant(const void* qx, const float* xs, const 
   if (rc) return rc;
   if (mtk == 0) return 0;
   if (!q2 || !s2) return -1;
-  if (rlu::launch_prefill_stream_act(qx, xs, wq, ws, sorted_ids, expert_ids, tiles, ntiles,
-                                     max_tiles, q2, s2, mtk, top_k, K, N, stream))
+  if (rlu::launch_prefill_stream_act(qx, xs, wq, ws, sorted_ids, expert_ids, nullptr, tiles,
+                                     ntiles, max_tiles, q2, s2, mtk, top_k, K, N, stream))
+    return -6;
+  return (int)hipGetLastError();
+}
+
+// ---- two aligns in one launch (a layer's resident slots and its non-resident experts) ------
+
+// The tile list of both aligns: align 0's tiles, then align 1's with bit 16 of the block
+// count set. tiles holds 2 (nb_max0 + nb_max1) ints.
+int rlu_moe_gemm_tiles_split(const int* expert_ids0, const int* num_post_pad0, int nb_max0,
+                             const int* expert_ids1, const int* num_post_pad1, int nb_max1,
+                             int* tiles, int* ntiles, hipStream_t stream) {
+  using namespace rlu::tiled;
+  if (nb_max0 <= 0 || nb_max0 > MAXNB || nb_max1 <= 0 || nb_max1 > MAXNB || !expert_ids0 ||
+      !num_post_pad0 || !expert_ids1 || !num_post_pad1 || !tiles || !ntiles)
+    return -1;
+  hipLaunchKernelGGL(tiles_k, dim3(1), dim3(TB_THR), 0, stream, expert_ids0, num_post_pad0,
+                     nb_max0, expert_ids1, num_post_pad1, nb_max1, tiles, ntiles);
+  return (int)hipGetLastError();
+}
+
+// rlu_moe_gemm_fp8blk_tiled over align 0 (weights wq0 / ws0) and align 1 (wq1 / ws1) in one
+// launch of the streamed kernel, from rlu_moe_gemm_tiles_split's list; the output equals the
+// two calls bit for bit. Built for the streamed kernel's shapes (K 2560 or 768, N % 256 == 0):
+// other shapes return -6 before anything else is checked (mtk = 0: a capability query).
+int rlu_moe_gemm_fp8blk_tiled_split(const void* qx, const float* xs, const void* wq0,
+                                    const float* ws0, const int* sorted_ids0,
+                                    const int* expert_ids0, const void* wq1, const float* ws1,
+                                    const int* sorted_ids1, const int* expert_ids1,
+                                    const int* tiles, const int* ntiles, int max_tiles,
+                                    const float* topk_weights, void* y, int mtk, int top_k,
+                                    int K, int N, hipStream_t stream) {
+  using namespace rlu::tiled;
+  if (!rlu::prefill_stream_built(K, N)) return -6;
+  const int rc = check_gemm_args(mtk, top_k, K, N, max_tiles, 0);
+  if (rc) return rc;
+  if (mtk == 0) return 0;
+  if (!qx || !xs || !wq0 || !ws0 || !sorted_ids0 || !expert_ids0 || !wq1 || !ws1 ||
+      !sorted_ids1 || !expert_ids1 || !tiles || !ntiles || !y)
+    return -1;
+  const rlu::PfSecond second{wq1, ws1, sorted_ids1, expert_ids1};
+  if (rlu::launch_prefill_stream(qx, xs, wq0, ws0, sorted_ids0, expert_ids0, &second, tiles,
+                                 ntiles, max_tiles, topk_weights, y, mtk, top_k, K, N, stream))
+    return -6;
+  return (int)hipGetLastError();
+}
+
+// rlu_moe_gemm_fp8blk_tiled_silu_quant over two aligns in one launch, as
+// rlu_moe_gemm_fp8blk_tiled_split; K = 2560 and N % 256 == 0, else -6 (mtk = 0: a query).
+int rlu_moe_gemm_fp8blk_tiled_split_silu_quant(const void* qx, const float* xs, const void* wq0,
+                                               const float* ws0, const int* sorted_ids0,
+                                               const int* expert_ids0, const void* wq1,
+                                               const float* ws1, const int* sorted_ids1,
+                                               const int* expert_ids1, const int* tiles,
+                                               const int* ntiles, int max_tiles, void* q2,
+                                               float* s2, int mtk, int top_k, int K, int N,
+                                               hipStream_t stream) {
+  using namespace rlu::tiled;
+  if (!rlu::prefill_stream_act_built(K, N)) return -6;
+  const int rc = check_gemm_args(mtk, top_k, K, N, max_tiles, 0);
+  if (rc) return rc;
+  if (mtk == 0) return 0;
+  if (!qx || !xs || !wq0 || !ws0 || !sorted_ids0 || !expert_ids0 || !wq1 || !ws1 ||
+      !sorted_ids1 || !expert_ids1 || !tiles || !ntiles || !q2 || !s2)
+    return -1;
+  const rlu::PfSecond second{wq1, ws1, sorted_ids1, expert_ids1};
+  if (rlu::launch_prefill_stream_act(qx, xs, wq0, ws0, sorted_ids0, expert_ids0, &second, tiles,
+                                     ntiles, max_tiles, q2, s2, mtk, top_k, K, N, stream))
     return -6;
   return (int)hipGetLastError();
 }

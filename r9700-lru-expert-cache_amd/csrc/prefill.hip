@@ -32,6 +32,11 @@
 //   * Items go to XCDs in contiguous ranges of tiles (workgroup b runs on XCD b % 8): the
 //     column groups of a tile run at the same time on CUs sharing one L2, which holds the
 //     tile's rows once.
+//   * One launch can cover two aligns over two weight sets (a layer's resident slots and the
+//     full tensor it reads non-resident experts from): the tile list then names the set of
+//     each tile (bit 16 of its block count), and an item takes its expert ids, sorted ids,
+//     weights and scales from that set. Both aligns index the same activation rows and write
+//     the same output.
 // Per step, acc = fma(mfma(a, b), xs * ws, acc) in ascending k from zero: the same sequence of
 // operations as moe_gemm_k with sk = 1, so the outputs are equal bit for bit.
 #include <hip/hip_runtime.h>
@@ -58,6 +63,11 @@ struct Args {
   const float* ws;
   const int* sorted_ids;
   const int* eids;
+  const uint8_t* wq1;            // the second set (tiles with set bit 1); the first when unused
+  const float* ws1;
+  const int* sorted_ids1;
+  const int* eids1;
+  bool two;                      // a two-set tile list
   const int* tiles;
   const int* ntiles;
   uint16_t* y;
@@ -70,7 +80,7 @@ struct Args {
 };
 
 struct Item {
-  int b0, nbk, e, n0;
+  int b0, nbk, e, n0, set;
 };
 
 typedef unsigned v2u __attribute__((ext_vector_type(2)));
@@ -111,11 +121,16 @@ struct Cfg {
 // whole in one item. The epilogue writes q2 [mtk, I] e4m3 and s2 [mtk, I / 128] instead of y,
 // computed from the bf16-rounded GEMM outputs exactly as silu_mul_quant_k computes them from
 // y (same silu, product and amax reduction, same rounding).
-template <int NK, int W, int S, int KC, int D, int BR, int BG, bool TWT, bool ACT>
+// TWO: the tile list covers two aligns (bit 16 of a tile's block count picks the set); the
+// one-set kernels take no second set, whose pointers would otherwise hold scalar registers for
+// the whole launch (in the gate_up kernels the extra registers spill: +5 us on 400).
+template <int NK, int W, int S, int KC, int D, int BR, int BG, bool TWT, bool ACT, bool TWO>
 __global__ __launch_bounds__(W * WAVE) void stream_k(
     const uint8_t* __restrict__ qx, const float* __restrict__ xs, const uint8_t* __restrict__ wq,
     const float* __restrict__ ws, const int* __restrict__ sorted_ids,
-    const int* __restrict__ eids, const int* __restrict__ tiles, const int* __restrict__ ntiles,
+    const int* __restrict__ eids, const uint8_t* __restrict__ wq1, const float* __restrict__ ws1,
+    const int* __restrict__ sorted_ids1, const int* __restrict__ eids1,
+    const int* __restrict__ tiles, const int* __restrict__ ntiles,
     uint16_t* __restrict__ y, const float* __restrict__ tw, uint8_t* __restrict__ q2,
     float* __restrict__ s2, int mtk, int top_k, int N) {
   using CF = Cfg<NK, W, S, KC, D, BR, BG>;
@@ -160,8 +175,10 @@ __global__ __launch_bounds__(W * WAVE) void stream_k(
     const int ti = it / ncg;
     Item r;
     r.b0 = tiles[2 * ti];
-    r.nbk = tiles[2 * ti + 1];
-    r.e = eids[r.b0];
+    const int nw = tiles[2 * ti + 1];              // block count | set << 16 (TWO)
+    r.nbk = TWO ? nw & 0xffff : nw;
+    r.set = TWO ? nw >> 16 : 0;
+    r.e = (r.set ? eids1 : eids)[r.b0];
     r.n0 = (it - ti * ncg) * C;
     return r;
   };
@@ -169,13 +186,14 @@ __global__ __launch_bounds__(W * WAVE) void stream_k(
   // h 1024 + lane 16 (the base and the step offset stay in scalar registers)
   auto wbase = [&](const Item& it) __attribute__((always_inline)) {
     return __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(wq + ((size_t)it.e * N + col0(it.n0)) * K), 0, S * 16 * K, BUF_WORD3);
+        (void*)((it.set ? wq1 : wq) + ((size_t)it.e * N + col0(it.n0)) * K), 0, S * 16 * K,
+        BUF_WORD3);
   };
   // the sorted id of row r16 of block blk of an item (mtk past the tile): one vector load,
   // issued at an item's start and used at its last chunk, so waiting for it costs nothing
   auto load_id = [&](const Item& it, int blk) __attribute__((always_inline)) {
     const bool in = blk < it.nbk;
-    const int v = sorted_ids[(it.b0 + (in ? blk : 0)) * 16 + r16];
+    const int v = (it.set ? sorted_ids1 : sorted_ids)[(it.b0 + (in ? blk : 0)) * 16 + r16];
     return in ? v : mtk;
   };
 
@@ -293,7 +311,8 @@ __global__ __launch_bounds__(W * WAVE) void stream_k(
         for (int s = 0; s < S; ++s) acc[bk][s] = v4f{0.f, 0.f, 0.f, 0.f};
       // the weight-block scales of this wave's strips, one per step: scalar loads (they never
       // enter the vector-memory counter the weight ring waits on)
-      const float* wsrow = ws + ((size_t)mA.e * (N / 128) + col0(mA.n0) / 128) * NK;
+      const float* wsrow =
+          (mA.set ? ws1 : ws) + ((size_t)mA.e * (N / 128) + col0(mA.n0) / 128) * NK;
       float wsr[NK];
 #pragma unroll
       for (int k = 0; k < NK; ++k) wsr[k] = wsrow[k];
@@ -471,10 +490,18 @@ static int launch_cfg(const Args& a, int max_tiles, hipStream_t stream) {
   int grid = device_cus() * OCC;
   if (grid > items) grid = items;
   if (grid >= NXCD) grid -= grid % NXCD;
+#define RLU_PF1(T, A, TW)                                                                     \
+  hipLaunchKernelGGL((stream_k<NK, W, S, KC, D, BR, BG, T, A, TW>), dim3(grid), dim3(W * WAVE), \
+                     CF::LDS, stream, a.qx, a.xs, a.wq, a.ws, a.sorted_ids, a.eids, a.wq1,      \
+                     a.ws1, a.sorted_ids1, a.eids1, a.tiles, a.ntiles, a.y, a.tw, a.q2, a.s2,   \
+                     a.mtk, a.top_k, a.N)
 #define RLU_PF(T, A)                                                                          \
-  hipLaunchKernelGGL((stream_k<NK, W, S, KC, D, BR, BG, T, A>), dim3(grid), dim3(W * WAVE),     \
-                     CF::LDS, stream, a.qx, a.xs, a.wq, a.ws, a.sorted_ids, a.eids, a.tiles,    \
-                     a.ntiles, a.y, a.tw, a.q2, a.s2, a.mtk, a.top_k, a.N)
+  do {                                                                                        \
+    if (a.two)                                                                                \
+      RLU_PF1(T, A, true);                                                                    \
+    else                                                                                      \
+      RLU_PF1(T, A, false);                                                                   \
+  } while (0)
   if constexpr (ACT_CFG)
     RLU_PF(false, true);
   else if (a.tw)
@@ -482,18 +509,34 @@ static int launch_cfg(const Args& a, int max_tiles, hipStream_t stream) {
   else
     RLU_PF(false, false);
 #undef RLU_PF
+#undef RLU_PF1
   return 0;
 }
 
 }  // namespace pf
 
+// the kernel arguments; without a second set, set 1 repeats set 0 (no tile names it)
+static pf::Args make_args(const void* qx, const float* xs, const void* wq, const float* ws,
+                          const int* sorted_ids, const int* expert_ids, const PfSecond* second,
+                          const int* tiles, const int* ntiles, const float* topk_weights,
+                          void* y, void* q2, float* s2, int mtk, int top_k, int N) {
+  const PfSecond one{wq, ws, sorted_ids, expert_ids};
+  const PfSecond& b = second ? *second : one;
+  return pf::Args{(const uint8_t*)qx, xs, (const uint8_t*)wq, ws, sorted_ids, expert_ids,
+                  (const uint8_t*)b.wq, b.ws, b.sorted_ids, b.expert_ids, second != nullptr,
+                  tiles, ntiles,
+                  (uint16_t*)y, topk_weights, (uint8_t*)q2, s2, mtk, top_k, N};
+}
+
+bool prefill_stream_built(int K, int N) { return (K == 2560 || K == 768) && N % 256 == 0; }
+
 int launch_prefill_stream(const void* qx, const float* xs, const void* wq, const float* ws,
-                          const int* sorted_ids, const int* expert_ids, const int* tiles,
-                          const int* ntiles, int max_tiles, const float* topk_weights, void* y,
-                          int mtk, int top_k, int K, int N, hipStream_t stream) {
-  const pf::Args a{(const uint8_t*)qx, xs,      (const uint8_t*)wq, ws,  sorted_ids,
-                   expert_ids,         tiles,   ntiles,             (uint16_t*)y,
-                   topk_weights,       nullptr, nullptr,            mtk, top_k, N};
+                          const int* sorted_ids, const int* expert_ids, const PfSecond* second,
+                          const int* tiles, const int* ntiles, int max_tiles,
+                          const float* topk_weights, void* y, int mtk, int top_k, int K, int N,
+                          hipStream_t stream) {
+  const pf::Args a = make_args(qx, xs, wq, ws, sorted_ids, expert_ids, second, tiles, ntiles,
+                               topk_weights, y, nullptr, nullptr, mtk, top_k, N);
   if (K == 2560) return pf::launch_cfg<20, 8, 2, 4, 5>(a, max_tiles, stream);
   if (K == 768) return pf::launch_cfg<6, 8, 2, 3, 6>(a, max_tiles, stream);
   return -1;
@@ -502,12 +545,12 @@ int launch_prefill_stream(const void* qx, const float* xs, const void* wq, const
 bool prefill_stream_act_built(int K, int N) { return K == 2560 && N % 256 == 0; }
 
 int launch_prefill_stream_act(const void* qx, const float* xs, const void* wq, const float* ws,
-                              const int* sorted_ids, const int* expert_ids, const int* tiles,
-                              const int* ntiles, int max_tiles, void* q2, float* s2, int mtk,
-                              int top_k, int K, int N, hipStream_t stream) {
-  const pf::Args a{(const uint8_t*)qx, xs,          (const uint8_t*)wq, ws,  sorted_ids,
-                   expert_ids,         tiles,       ntiles,             nullptr,
-                   nullptr,            (uint8_t*)q2, s2,                mtk, top_k, N};
+                              const int* sorted_ids, const int* expert_ids,
+                              const PfSecond* second, const int* tiles, const int* ntiles,
+                              int max_tiles, void* q2, float* s2, int mtk, int top_k, int K,
+                              int N, hipStream_t stream) {
+  const pf::Args a = make_args(qx, xs, wq, ws, sorted_ids, expert_ids, second, tiles, ntiles,
+                               nullptr, nullptr, q2, s2, mtk, top_k, N);
   if (K == 2560) return pf::launch_cfg<20, 8, 2, 4, 4, true>(a, max_tiles, stream);
   return -1;
 }

@@ -172,6 +172,16 @@ class LruMoELayer:
             self.tiles = {t.data_ptr(): torch.empty(2 * t.numel() + 1, dtype=torch.int32,
                                                     device=dev)
                           for t in (self.align[1], self.align[4], self.eids_res, self.eids_new)}
+            # where the streamed kernel is built for both GEMMs, a GEMM over the hot align (or
+            # the overlap's resident bucket) and the cold align is one launch over one tile
+            # list of both (an empty cold align then costs no launch of its own)
+            self.pf_split = (ops.moe_gemm_tiled_split_built(self.H, self.N1) and
+                             ops.moe_gemm_tiled_split_built(self.I, self.H))
+            ec = self.align[4]
+            self.split_tiles = {
+                (t.data_ptr(), ec.data_ptr()): torch.empty(2 * (t.numel() + ec.numel()) + 1,
+                                                           dtype=torch.int32, device=dev)
+                for t in (self.align[1], self.eids_res)} if self.pf_split else {}
             self.tiles_built = set()
 
     @classmethod
@@ -257,6 +267,11 @@ class LruMoELayer:
         eh = eh0 if eh is None else eh
         if self.prefill:
             full = self.full.tensors()
+            if self.pf_split:
+                ops.moe_gemm_tiled_split(y, qx, xs, slot_w, slot_s, (sh, eh, nh), full[part],
+                                         full[part + 1], (sc, ec, nc), tw, y.shape[0], top_k,
+                                         tiles=self._split_tiles_of(eh, nh), tiles_ready=True)
+                return
             self._gemm_tiled(y, qx, xs, slot_w, slot_s, sh, eh, nh, tw, top_k)
             self._gemm_tiled(y, qx, xs, full[part], full[part + 1], sc, ec, nc, tw, top_k)
             return
@@ -290,6 +305,16 @@ class LruMoELayer:
             self.tiles_built.add(key)
         return self.tiles[key]
 
+    def _split_tiles_of(self, eh, nh):
+        """The tile list of hot block expert ids eh and the cold align, built on its first use
+        in a step."""
+        ec, nc = self.align[4], self.align[5]
+        key = (eh.data_ptr(), ec.data_ptr())
+        if key not in self.tiles_built:
+            ops.moe_gemm_tiles_split((eh, nh), (ec, nc), self.split_tiles[key])
+            self.tiles_built.add(key)
+        return self.split_tiles[key]
+
     def _gemm_tiled(self, y, qx, xs, w, s, sorted_ids, eids, npad, tw, top_k):
         ops.moe_gemm_tiled(y, qx, xs, w, s, sorted_ids, eids, npad, tw, y.shape[0], top_k,
                            tiles=self._tiles_of(eids, npad), tiles_ready=True)
@@ -311,8 +336,14 @@ class LruMoELayer:
             return
         if self.fuse_act:
             sh, eh0, nh, sc, ec, nc = self.align
-            for w, s, al in (((self.slots.w13, self.slots.s13, (sh, eh0 if eh is None else eh,
-                                                               nh)),) +
+            eh = eh0 if eh is None else eh
+            if cold and self.pf_split:
+                ops.moe_gemm_tiled_split_silu_quant(
+                    self.q2, self.s2, self.qx, self.xs, self.slots.w13, self.slots.s13,
+                    (sh, eh, nh), self.full.w13, self.full.s13, (sc, ec, nc), self.mtk,
+                    self.top_k, tiles=self._split_tiles_of(eh, nh), tiles_ready=True)
+                return
+            for w, s, al in (((self.slots.w13, self.slots.s13, (sh, eh, nh)),) +
                              (((self.full.w13, self.full.s13, (sc, ec, nc)),) if cold else ())):
                 ops.moe_gemm_tiled_silu_quant(self.q2, self.s2, self.qx, self.xs, w, s, *al,
                                               self.mtk, self.top_k,

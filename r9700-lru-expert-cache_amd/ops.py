@@ -380,6 +380,84 @@ def moe_gemm_tiled_silu_quant(q2: torch.Tensor, s2: torch.Tensor, qx: torch.Tens
     check(rc, "rlu_moe_gemm_fp8blk_tiled_silu_quant")
 
 
+# ---- two aligns in one launch: a layer's resident slots (align 0) and its full tensor --------
+def moe_gemm_tiles_split(al0, al1, out: torch.Tensor | None = None) -> torch.Tensor:
+    """The tile list of two aligns, al = (expert_ids, num_post_pad): int32 [2 (nb0 + nb1) + 1]
+    = align 0's tiles (first block, block count), then align 1's with bit 16 of the block
+    count set, then the tile count at the end."""
+    (e0, n0), (e1, n1) = al0, al1
+    nb = e0.numel() + e1.numel()
+    ws = torch.empty(2 * nb + 1, dtype=torch.int32, device=e0.device) if out is None else out
+    assert ws.numel() == 2 * nb + 1 and ws.dtype == torch.int32
+    rc = lib().rlu_moe_gemm_tiles_split(_p(e0), _p(n0), e0.numel(), _p(e1), _p(n1), e1.numel(),
+                                        _p(ws), _P(ws.data_ptr() + 8 * nb), _P(stream_ptr()))
+    check(rc, "rlu_moe_gemm_tiles_split")
+    return ws
+
+
+def _split_tiles(al0, al1, tiles, ready):
+    nb = al0[1].numel() + al1[1].numel()
+    if ready:
+        assert tiles is not None and tiles.numel() == 2 * nb + 1 and tiles.dtype == torch.int32, \
+            "tiles_ready needs the aligns' split tile list"
+        return tiles, nb
+    return moe_gemm_tiles_split(al0[1:], al1[1:], tiles), nb
+
+
+def moe_gemm_tiled_split_built(K: int, N: int) -> bool:
+    """Whether moe_gemm_tiled_split has a kernel for weights [*, N, K] (a zero-row call:
+    nothing is launched)."""
+    rc = lib().rlu_moe_gemm_fp8blk_tiled_split(*([_P(0)] * 12), 1, _P(0), _P(0), 0, 1, K, N,
+                                               _P(0))
+    return rc == 0
+
+
+def moe_gemm_tiled_split(y: torch.Tensor, qx: torch.Tensor, x_scale: torch.Tensor,
+                         w0: torch.Tensor, s0: torch.Tensor, al0, w1: torch.Tensor,
+                         s1: torch.Tensor, al1, topk_weights: torch.Tensor | None, mtk: int,
+                         top_k: int, tiles: torch.Tensor | None = None,
+                         tiles_ready: bool = False) -> None:
+    """moe_gemm_tiled over two aligns in one launch of the streamed kernel: al0 = (sorted_ids,
+    expert_ids, num_post_pad) over weights w0 / s0 (a layer's resident slots) and al1 over w1 /
+    s1 (its full tensor, device or pinned host memory), both indexing the rows of qx and
+    writing y. Equals moe_gemm_tiled on each align bit for bit. Raises for shapes without a
+    kernel (moe_gemm_tiled_split_built). tiles: int32 workspace of 2 (nb0 + nb1) + 1 entries;
+    with tiles_ready it holds moe_gemm_tiles_split of these aligns and is not rebuilt."""
+    K = qx.shape[1]
+    N = w0.shape[1]
+    assert y.shape == (mtk, N) and y.dtype == torch.bfloat16 and y.is_contiguous()
+    assert qx.dtype == FP8 and w0.dtype == FP8 and w1.dtype == FP8
+    assert w0.shape[1:] == (N, K) and w1.shape[1:] == (N, K)
+    tiles, nb = _split_tiles(al0, al1, tiles, tiles_ready)
+    rc = lib().rlu_moe_gemm_fp8blk_tiled_split(
+        _p(qx), _p(x_scale), _P(device_ptr(w0)), _P(device_ptr(s0)), _p(al0[0]), _p(al0[1]),
+        _P(device_ptr(w1)), _P(device_ptr(s1)), _p(al1[0]), _p(al1[1]), _p(tiles),
+        _P(tiles.data_ptr() + 8 * nb), nb, _p(topk_weights), _p(y), mtk, top_k, K, N,
+        _P(stream_ptr()))
+    check(rc, "rlu_moe_gemm_fp8blk_tiled_split")
+
+
+def moe_gemm_tiled_split_silu_quant(q2: torch.Tensor, s2: torch.Tensor, qx: torch.Tensor,
+                                    x_scale: torch.Tensor, w0: torch.Tensor, s0: torch.Tensor,
+                                    al0, w1: torch.Tensor, s1: torch.Tensor, al1, mtk: int,
+                                    top_k: int, tiles: torch.Tensor | None = None,
+                                    tiles_ready: bool = False) -> None:
+    """moe_gemm_tiled_silu_quant over two aligns in one launch, as moe_gemm_tiled_split:
+    equals moe_gemm_tiled_silu_quant on each align bit for bit."""
+    K = qx.shape[1]
+    N = w0.shape[1]
+    assert q2.shape == (mtk, N // 2) and q2.dtype == FP8 and q2.is_contiguous()
+    assert s2.shape == (mtk, N // 256) and s2.dtype == torch.float32 and s2.is_contiguous()
+    assert qx.dtype == FP8 and w0.dtype == FP8 and w1.dtype == FP8
+    assert w0.shape[1:] == (N, K) and w1.shape[1:] == (N, K)
+    tiles, nb = _split_tiles(al0, al1, tiles, tiles_ready)
+    rc = lib().rlu_moe_gemm_fp8blk_tiled_split_silu_quant(
+        _p(qx), _p(x_scale), _P(device_ptr(w0)), _P(device_ptr(s0)), _p(al0[0]), _p(al0[1]),
+        _P(device_ptr(w1)), _P(device_ptr(s1)), _p(al1[0]), _p(al1[1]), _p(tiles),
+        _P(tiles.data_ptr() + 8 * nb), nb, _p(q2), _p(s2), mtk, top_k, K, N, _P(stream_ptr()))
+    check(rc, "rlu_moe_gemm_fp8blk_tiled_split_silu_quant")
+
+
 NOALLOC_MAX_BLOCKS = 8192      # the scratch tile list's capacity (131072 sorted ids)
 
 

@@ -946,6 +946,126 @@ def test_moe_gemm_tiled_silu_quant_fused(ops, layer, M):
             layer["w2t"], layer["w2s"], *al, mtk, 1)
 
 
+# ---- the prefill GEMMs over a layer's two aligns in one launch -------------------------------
+def split_case(layer, M, hot_share, seed):
+    """A hot / cold split of prefill routing over the layer's 40 experts: every hot_share-th
+    routed expert resident in a slot (0: only an expert no row routes to, so the hot align is
+    empty; -1: every routed expert, so the cold align is empty). Returns the routing, the two
+    aligns (host arrays) and the slot tensors' expert order."""
+    E = layer["E"]
+    ids = routing(M, 10, E - 1 if hot_share == 0 else E, seed=seed)   # 0: expert E - 1 unused
+    used = sorted(set(ids.reshape(-1).tolist()))
+    if hot_share > 0:
+        hot_experts = used[::hot_share]
+    elif hot_share == 0:
+        hot_experts = [E - 1]
+    else:
+        hot_experts = used
+    al = align_all(ids, E, {e: i for i, e in enumerate(hot_experts)})
+    return ids, al, hot_experts
+
+
+@pytest.mark.parametrize("M,hot_share", [(256, 2), (600, 3), (37, 2), (256, 0), (256, -1)])
+def test_moe_gemm_tile_list_split(ops, layer, M, hot_share):
+    """The tile list of two aligns: the hot align's tiles, then the cold align's with bit 16
+    of the block count set, then the count -- each list as tiles_ref walks it."""
+    _, al, _ = split_case(layer, M, hot_share, seed=M + 11)
+    sh, eh, nh, sc, ec, nc = al
+    e_h, n_h, e_c, n_c = to_dev_i32(eh, nh, ec, nc)
+    gpu_case(f"split tile list M={M} hot_share={hot_share}")
+    tl = ops.moe_gemm_tiles_split((e_h, n_h), (e_c, n_c))
+    torch.cuda.synchronize()
+    got = tl.cpu().numpy()
+    want = tiles_ref(eh, nh[0]) + [(b, n | 1 << 16) for b, n in tiles_ref(ec, nc[0])]
+    nt = int(got[-1])
+    assert nt == len(want)
+    assert [tuple(x) for x in got[:2 * nt].reshape(-1, 2)] == want
+    assert len(got) == 2 * (len(eh) + len(ec)) + 1
+
+
+@pytest.mark.parametrize("M,hot_share,pinned", [(256, 2, False), (600, 3, True), (37, 2, False),
+                                                (256, 0, False), (256, -1, True)])
+def test_moe_gemm_tiled_split_equals_two_calls(ops, layer, M, hot_share, pinned):
+    """moe_gemm_tiled_split over a hot align (slot weights) and a cold align (the full tensor,
+    in device or pinned host memory) in one launch equals moe_gemm_tiled on each align bit
+    for bit: gate_up, down with routed weights, and gate_up with SiLU-mul-quant."""
+    E, H, I = layer["E"], layer["H"], layer["I"]
+    ids, al, hot_experts = split_case(layer, M, hot_share, seed=M + 13)
+    mtk = ids.size
+    sh, eh, nh, sc, ec, nc = to_dev_i32(*al)
+    hot, cold = (sh, eh, nh), (sc, ec, nc)
+    idx = torch.tensor(hot_experts, device=DEV)
+
+    def full(t):
+        if not pinned:
+            return t
+        h = torch.empty(t.shape, dtype=t.dtype, pin_memory=True)
+        h.copy_(t)
+        return h
+    rng = np.random.default_rng(M + 17)
+    x = fp8.bf16_round(rng.standard_normal((M, H)).astype(np.float32))
+    qx, xs = fp8.group_quant(x, 128)
+    qx_t = torch.from_numpy(qx).to(DEV).view(torch.float8_e4m3fn)
+    xs_t = torch.from_numpy(xs).to(DEV)
+    a = fp8.bf16_round(rng.standard_normal((mtk, I)).astype(np.float32))
+    q2, s2 = fp8.group_quant(a, 128)
+    q2_t = torch.from_numpy(q2).to(DEV).view(torch.float8_e4m3fn)
+    s2_t = torch.from_numpy(s2).to(DEV)
+    tw = torch.from_numpy(rng.random(mtk).astype(np.float32)).to(DEV)
+    for name, w, s, xq, xsc, twt, tk, N in (
+            ("gate_up", layer["w13t"], layer["w13s"], qx_t, xs_t, None, 10, 2 * I),
+            ("down", layer["w2t"], layer["w2s"], q2_t, s2_t, tw, 1, H)):
+        sw, ss = w[idx].contiguous(), s[idx].contiguous()
+        fw, fs = full(w), full(s)
+        y2 = torch.full((mtk, N), float("nan"), dtype=torch.bfloat16, device=DEV)
+        gpu_case(f"split tiled {name} M={M} hot_share={hot_share} pinned={pinned}: two calls")
+        ops.moe_gemm_tiled(y2, xq, xsc, sw, ss, *hot, twt, mtk, tk)
+        ops.moe_gemm_tiled(y2, xq, xsc, fw, fs, *cold, twt, mtk, tk)
+        y1 = torch.full_like(y2, float("nan"))
+        gpu_case(f"split tiled {name} M={M} hot_share={hot_share} pinned={pinned}: one launch")
+        ops.moe_gemm_tiled_split(y1, xq, xsc, sw, ss, hot, fw, fs, cold, twt, mtk, tk)
+        torch.cuda.synchronize()
+        assert not torch.isnan(y1).any()
+        assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+        if name == "gate_up":
+            qa = torch.full((mtk, I), 0x7F, dtype=torch.uint8, device=DEV).view(ops.FP8)
+            sa = torch.full((mtk, I // 128), float("nan"), device=DEV)
+            qb = torch.full_like(qa.view(torch.uint8), 0x7F).view(ops.FP8)
+            sb = torch.full_like(sa, 1.0)
+            gpu_case(f"split tiled gate_up + silu-mul-quant M={M} hot_share={hot_share}")
+            ops.moe_gemm_tiled_silu_quant(qa, sa, xq, xsc, sw, ss, *hot, mtk, tk)
+            ops.moe_gemm_tiled_silu_quant(qa, sa, xq, xsc, fw, fs, *cold, mtk, tk)
+            ops.moe_gemm_tiled_split_silu_quant(qb, sb, xq, xsc, sw, ss, hot, fw, fs, cold, mtk,
+                                                tk)
+            torch.cuda.synchronize()
+            assert not torch.isnan(sa).any()
+            assert torch.equal(qa.view(torch.uint8), qb.view(torch.uint8))
+            assert torch.equal(sa.view(torch.int32), sb.view(torch.int32))
+
+
+def test_moe_gemm_tiled_split_return_codes(pkg, ops):
+    """Built for the streamed kernel's shapes only (-6 otherwise, before any other check);
+    null pointers -1; the tile builder's limits."""
+    assert ops.moe_gemm_tiled_split_built(2560, 1536) and ops.moe_gemm_tiled_split_built(768, 2560)
+    assert not ops.moe_gemm_tiled_split_built(1024, 1536)
+    assert not ops.moe_gemm_tiled_split_built(2560, 1536 + 128)
+    P = ctypes.c_void_p
+    lib = pkg.lib()
+    s = P(torch.cuda.current_stream().cuda_stream)
+    z = [P(0)] * 12
+    assert lib.rlu_moe_gemm_fp8blk_tiled_split_silu_quant(*z, 1, P(0), P(0), 0, 1, 768, 2560,
+                                                          s) == -6
+    assert lib.rlu_moe_gemm_fp8blk_tiled_split(*z, 1, P(0), P(0), 20, 10, 2560, 1536, s) == -1
+    assert lib.rlu_moe_gemm_fp8blk_tiled_split_silu_quant(*z, 1, P(0), P(0), 20, 10, 2560, 1536,
+                                                          s) == -1
+    assert lib.rlu_moe_gemm_fp8blk_tiled_split(*z, 0, P(0), P(0), 20, 10, 2560, 1536, s) == -1
+    t = torch.zeros(64, dtype=torch.int32, device=DEV)
+    p = P(t.data_ptr())
+    assert lib.rlu_moe_gemm_tiles_split(p, p, 4, p, p, 8193, p, p, s) == -1
+    assert lib.rlu_moe_gemm_tiles_split(p, p, 0, p, p, 4, p, p, s) == -1
+    assert lib.rlu_moe_gemm_tiles_split(p, p, 4, P(0), p, 4, p, p, s) == -1
+
+
 def test_moe_gemm_tiled_row_contract_and_graph(ops, layer):
     """A block of expert -1 is skipped (its rows stay NaN); graph replay equals eager."""
     E, H, I = layer["E"], layer["H"], layer["I"]
