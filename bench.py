@@ -1111,6 +1111,10 @@ def main():
     ap.add_argument("--counter-probe", action="store_true",
                     help="for LDS / MFMA counter runs: the fused LRU kernel in the insert storm "
                          "and the prefill grouped GEMMs, then exit")
+    ap.add_argument("--prefill-leg", action="store_true",
+                    help="only the prefill leg (4096 tokens: the GEMMs alone, then the layer "
+                         "steps with every expert resident and with 257 slots); prints its "
+                         "figures")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="for counter runs: one eager B=4 step of the 52 layers, their 104 "
                          "grouped-GEMM launches once more, then a 256 MiB device copy (the "
@@ -1131,6 +1135,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.counter_probe:
         counter_probe(torch, pkg, dev)
+        return
+    if args.prefill_leg:
+        print(json.dumps({"prefill_4096": prefill_gemm(torch, pkg, dev)}), flush=True)
         return
     t_setup = time.perf_counter()
     log("generating 512 fp8 experts")
