@@ -205,7 +205,8 @@ int rlu_moe_gemm_tiles(const int* expert_ids, const int* num_post_pad, int nb_ma
  * persistent, one workgroup per CU walking (tile, 256-column strip) items with the weight stream
  * kept in flight across items), else the general tiled kernel at 2 workgroups per CU; wv in
  * 1..16 forces the general kernel at wv workgroups per CU. Every choice gives the same bits.
- * Returns -1 / -2 / -5 as above. */
+ * Returns -1 (bad sizes, or a NULL pointer other than topk_weights when mtk > 0), -2 (K % 128
+ * or N % 256), -5 (wv outside 0..16). */
 int rlu_moe_gemm_fp8blk_tiled(const void* qx, const float* xs, const void* wq, const float* ws,
                               const int* sorted_ids, const int* expert_ids, const int* tiles,
                               const int* ntiles, int max_tiles, const float* topk_weights,

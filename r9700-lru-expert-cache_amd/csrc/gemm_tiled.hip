@@ -344,6 +344,8 @@ int rlu_moe_gemm_fp8blk_tiled(const void* qx, const float* xs, const void* wq, c
   const int rc = check_gemm_args(mtk, top_k, K, N, max_tiles, wv);
   if (rc) return rc;
   if (mtk == 0) return 0;
+  if (!qx || !xs || !wq || !ws || !sorted_ids || !expert_ids || !tiles || !ntiles || !y)
+    return -1;
   launch_tiled(qx, xs, wq, ws, sorted_ids, expert_ids, tiles, ntiles, max_tiles, topk_weights, y,
                mtk, top_k, K, N, wv, stream);
   return (int)hipGetLastError();
@@ -362,6 +364,7 @@ int rlu_moe_gemm_fp8blk_tiled_noalloc(const void* qx, const float* xs, const voi
   if (rc) return rc;
   if (nb > MAXNB) return -7;                        // beyond the scratch tile list
   if (mtk == 0) return 0;
+  if (!qx || !xs || !wq || !ws || !sorted_ids || !y) return -1;
   int* ws_tiles = nullptr;
   const int e = scratch_ptr(&ws_tiles);
   if (e) return e;
@@ -389,7 +392,8 @@ int rlu_moe_gemm_fp8blk_tiled_silu_quant(const void* qx, const float* xs, const 
   const int rc = check_gemm_args(mtk, top_k, K, N, max_tiles, 0);
   if (rc) return rc;
   if (mtk == 0) return 0;
-  if (!q2 || !s2) return -1;
+  if (!qx || !xs || !wq || !ws || !sorted_ids || !expert_ids || !tiles || !ntiles || !q2 || !s2)
+    return -1;
   if (rlu::launch_prefill_stream_act(qx, xs, wq, ws, sorted_ids, expert_ids, nullptr, tiles,
                                      ntiles, max_tiles, q2, s2, mtk, top_k, K, N, stream))
     return -6;

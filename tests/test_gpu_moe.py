@@ -1059,6 +1059,13 @@ def test_moe_gemm_tiled_split_return_codes(pkg, ops):
     assert lib.rlu_moe_gemm_fp8blk_tiled_split_silu_quant(*z, 1, P(0), P(0), 20, 10, 2560, 1536,
                                                           s) == -1
     assert lib.rlu_moe_gemm_fp8blk_tiled_split(*z, 0, P(0), P(0), 20, 10, 2560, 1536, s) == -1
+    # the one-align entries: a NULL operand is -1 before anything is launched (mtk > 0)
+    z8 = [P(0)] * 8
+    assert lib.rlu_moe_gemm_fp8blk_tiled(*z8, 1, P(0), P(0), 20, 10, 2560, 1536, 0, s) == -1
+    assert lib.rlu_moe_gemm_fp8blk_tiled_silu_quant(*z8, 1, P(0), P(0), 20, 10, 2560, 1536,
+                                                    s) == -1
+    assert lib.rlu_moe_gemm_fp8blk_tiled_noalloc(*([P(0)] * 5), P(1), P(1), 1, P(0), P(0), 20,
+                                                 10, 2560, 1536, 0, s) == -1
     t = torch.zeros(64, dtype=torch.int32, device=DEV)
     p = P(t.data_ptr())
     assert lib.rlu_moe_gemm_tiles_split(p, p, 4, p, p, 8193, p, p, s) == -1
