@@ -332,6 +332,7 @@ int r4d_gemm_moe_fp8blk_nt_b16(const void* qx, const float* xs, const void* wq,
   if (rlu::bad_sk(K, sk)) return -4;
   if (wv < 0 || wv > 16) return -5;
   if (mtk == 0) return 0;
+  if (!qx || !xs || !wq || !ws || !y || !sorted_ids || !expert_ids || !num_post_pad) return -1;
   const int nb = (em + 15) / 16;
   const int items = nb * (N / (16 * npw));
   const int grid = rlu::grid_for(items, sk, wv);
@@ -358,6 +359,9 @@ int rlu_moe_gemm_split(const void* qx, const float* xs, const void* wq_hot, cons
   if (rlu::bad_sk(K, sk)) return -4;
   if (wv < 0 || wv > 16) return -5;
   if (mtk == 0) return 0;
+  if (!qx || !xs || !wq_hot || !ws_hot || !sorted_hot || !eids_hot || !npad_hot || !wq || !ws ||
+      !sorted_cold || !eids_cold || !npad_cold || !y)
+    return -1;
   // live blocks are numbered densely (hot list, then cold list) and each holds at least one of
   // the mtk rows, so there are at most min(2 ceil(em / 16), mtk) of them: the grid covers no
   // more (workgroups past the live ones still cost a dispatch and a scalar load each)
@@ -440,6 +444,7 @@ int rlu_gemm_fp8blk_m16(const void* qx, const float* xs, const void* w, const fl
   const int sk = rlu::pick_sk(K / 128, 0);
   if (rlu::bad_sk(K, sk)) return -4;
   if (wv < 0 || wv > 16) return -5;
+  if (!qx || !xs || !w || !ws || !y) return -1;
   const int items = N / (16 * npw);
   const int grid = rlu::grid_for(items, sk, wv);
   const rlu::WSet s0{(const uint8_t*)w, ws, nullptr, nullptr, nullptr};

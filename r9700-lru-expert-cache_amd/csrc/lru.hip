@@ -1204,6 +1204,7 @@ int rlu_lru_split_fresh(const int* eids_hot, int nb, const int* miss, const int*
                         hipStream_t stream) {
   if (nb < 0 || miss_cap < 0 || S <= 0 || S > rlu::MAXS) return -1;
   if (nb == 0) return 0;
+  if (!eids_hot || !miss || !n_miss || !eids_res || !eids_new) return -1;
   hipLaunchKernelGGL(rlu::split_fresh_k, dim3(1), dim3(rlu::NT), 0, stream, eids_hot, nb, miss,
                      n_miss, miss_cap, S, eids_res, eids_new);
   return (int)hipGetLastError();

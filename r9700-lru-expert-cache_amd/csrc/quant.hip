@@ -249,6 +249,7 @@ int rlu_quant_fp8_group(const void* x, int rows, int K, int ldx, int group, void
   if (!(group == 0 || (group == 128 && K % 128 == 0))) return -2;
   if (group == 0 && K > rlu::QT * 8 * 64) return -3;
   if (rows == 0) return 0;
+  if (!x || !q || !scale) return -1;
   hipLaunchKernelGGL(rlu::group_quant_k, dim3(rows), dim3(rlu::QT), 0, stream,
                      (const uint16_t*)x, K, ldx, group, (uint8_t*)q, scale);
   return (int)hipGetLastError();
@@ -260,6 +261,7 @@ int rlu_silu_mul_quant(const void* x, int rows, int d, int ldx, int group, void*
   if (!(group == 0 || (group == 128 && d % 128 == 0))) return -2;
   if (group == 0 && d > rlu::QT * 8 * 4) return -3;
   if (rows == 0) return 0;
+  if (!x || !q || !scale) return -1;                // act is optional
   if (group == 128) {
     const long long units = (long long)rows * (d / 128);
     long long grid = (units + rlu::SQ_UNITS - 1) / rlu::SQ_UNITS;
@@ -278,6 +280,7 @@ int rlu_silu_mul_quant(const void* x, int rows, int d, int ldx, int group, void*
 int rlu_moe_sum(const void* in, int M, int top_k, int H, void* out, hipStream_t stream) {
   if (M < 0 || top_k <= 0 || H <= 0 || H % 8) return -1;
   if (M == 0) return 0;
+  if (!in || !out) return -1;
   hipLaunchKernelGGL(rlu::moe_sum_k, dim3(M, (H + rlu::SUM_THR * 8 - 1) / (rlu::SUM_THR * 8)),
                      dim3(rlu::SUM_THR), 0, stream, (const uint16_t*)in, top_k, H,
                      (uint16_t*)out);

@@ -252,6 +252,7 @@ int rlu_gemm_w4_m16(const void* x, int M, int K, const void* wq, const unsigned*
   if (M < 1 || M > 16 || K <= 0 || N <= 0 || wv < 0 || wv > 16) return -1;
   if (K % 128 || N % (16 * SS) || K > MAXK) return -2;
   if ((long long)N * K / 2 >= (1LL << 31)) return -2;   // buffer byte offsets are 32-bit
+  if (!x || !wq || !sz || !y) return -1;
   const int G = K / 128;
   const int skw = G % 4 == 0 ? 4 : G % 2 == 0 ? 2 : 1;
   const int gq = G / skw;

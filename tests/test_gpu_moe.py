@@ -389,6 +389,24 @@ def test_moe_gemm_return_codes(ops, layer):
                                        10, 10, wv, sk, npw)
 
 
+def test_entry_points_refuse_null_operands(pkg):
+    """With valid sizes and NULL operands every compute entry point returns -1 before it
+    launches anything (a NULL would otherwise fault on the device)."""
+    P = ctypes.c_void_p
+    lib = pkg.lib()
+    s = P(torch.cuda.current_stream().cuda_stream)
+    z = P(0)
+    assert lib.rlu_quant_fp8_group(z, 4, 256, 256, 128, z, z, s) == -1
+    assert lib.rlu_silu_mul_quant(z, 4, 256, 512, 128, z, z, z, s) == -1
+    assert lib.rlu_moe_sum(z, 4, 10, 2560, z, s) == -1
+    assert lib.r4d_gemm_moe_fp8blk_nt_b16(*([z] * 10), 16, 20, 10, 2560, 1536, 0, 0, 2, s) == -1
+    assert lib.rlu_moe_gemm_split(*([z] * 14), 16, 20, 10, 2560, 1536, 0, 0, 2, s) == -1
+    assert lib.rlu_gemm_fp8blk_m16(*([z] * 5), 1, 1536, 2560, 0, 2, s) == -1
+    assert lib.rlu_gemm_w4_m16(z, 1, 2560, z, z, z, 1536, 0, s) == -1
+    assert lib.rlu_lru_split_fresh(z, 4, z, z, 64, 257, z, z, s) == -1
+    torch.cuda.synchronize()
+
+
 # ---- fp8 lm_head -----------------------------------------------------------------------------
 @pytest.fixture(scope="module")
 def lm_head(ops):
